@@ -1,0 +1,252 @@
+/*
+ * jacq_kivi.h -- C ABI of the MI355X (gfx950) int4-KIVI paged KV-cache library
+ * (libjacq_kivi.so).
+ *
+ * Two groups of entry points:
+ *
+ *  1. The reference's callable launch contract, ABI v1, unchanged: same
+ *     symbol names, argument order, block-table format, packed-int4 code
+ *     layout and fp16 scale/zero layout.  Geometry is fixed per symbol, as in
+ *     the reference (NH=40, NKV=8, HD=128, page=group=32, residual=128,
+ *     124-entry block table; the *_tp2_local symbols use NH=20, NKV=4).
+ *     Citations are to the reference repository.
+ *
+ *  2. Additive runtime-geometry entry points (jacq_kivi_*): batches of
+ *     sequences, page size 16 or 32 with a 32-token quantisation group, head
+ *     dim 64 or 128, any GQA ratio up to 16, any residual window that is a
+ *     multiple of the group, and block tables wider than 124 entries.  Per
+ *     sequence they compute exactly what the v1 symbols compute.
+ *
+ * Conventions (both groups):
+ *  - every pointer is caller-owned device memory; the v1 symbols never
+ *    allocate; the jacq_kivi_* symbols allocate only the split-K workspace,
+ *    once per device, when the caller passes none;
+ *  - every call is asynchronous on `stream`; a cache write followed by a
+ *    decode on the same stream is ordered;
+ *  - fp16 tensors are IEEE binary16 bit patterns (jacq_half_t), bit
+ *    compatible with __half / torch.float16.
+ *
+ * Tensor layouts (P = page size, G = 32 = quantisation group, RS = R + G):
+ *   K_CODE_PAGES, V_CODE_PAGES  uint8  [num_pages, NKV, P, HD/2]
+ *                               channel d of token t: byte d/2, low nibble
+ *                               for even d, high nibble for odd d
+ *   K_SCALE_PAGES, K_ZERO_PAGES fp16   [num_pages, NKV, HD]     (per group,
+ *                               written to every page of the group)
+ *   V_SCALE_PAGES, V_ZERO_PAGES fp16   [num_pages, NKV, P, HD/G]
+ *   K/V_RESIDUAL_SCRATCH        fp16   [NKV, RS, HD] per sequence
+ *   BLOCK_TABLE                 int32  logical page -> physical page
+ */
+#ifndef JACQ_KIVI_H
+#define JACQ_KIVI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t jacq_half_t;
+
+/* Version of the reference launch contract the v1 symbols implement
+ * (integrations/vllm_kivi/abi.py:36, JACQ_KIVI_ABI_VERSION = 1). */
+#define JACQ_KIVI_ABI_VERSION 1
+/* Version of the additive jacq_kivi_* runtime-geometry surface. */
+#define JACQ_KIVI_EXT_VERSION 1
+
+/* ------------------------------------------------------------------------ */
+/* 1. Reference contract, ABI v1                                             */
+/* ------------------------------------------------------------------------ */
+
+/* Paged KIVI decode of one query token for one sequence; O [NH,HD] fp32.
+ * Replaces jac_launch, crates/jac-codegen-cuda/tests/snapshots/kernels/
+ * decode_attention_kivi_paged_library_flash.cu:164-172 (declared at
+ * integrations/vllm_kivi/source_patch.py:570-576). */
+void jac_launch(const jacq_half_t* Q, const int32_t* BLOCK_TABLE,
+                const uint8_t* K_CODE_PAGES, const jacq_half_t* K_SCALE_PAGES,
+                const jacq_half_t* K_ZERO_PAGES, const uint8_t* V_CODE_PAGES,
+                const jacq_half_t* V_SCALE_PAGES, const jacq_half_t* V_ZERO_PAGES,
+                const jacq_half_t* K_RESIDUAL_SCRATCH, const jacq_half_t* V_RESIDUAL_SCRATCH,
+                int SEQ_LEN, float* O, hipStream_t stream);
+
+/* TP=2 local-rank geometry NH=20/NKV=4; source_patch.py:578-584. */
+void jac_launch_tp2_local(const jacq_half_t* Q, const int32_t* BLOCK_TABLE,
+                          const uint8_t* K_CODE_PAGES, const jacq_half_t* K_SCALE_PAGES,
+                          const jacq_half_t* K_ZERO_PAGES, const uint8_t* V_CODE_PAGES,
+                          const jacq_half_t* V_SCALE_PAGES, const jacq_half_t* V_ZERO_PAGES,
+                          const jacq_half_t* K_RESIDUAL_SCRATCH,
+                          const jacq_half_t* V_RESIDUAL_SCRATCH, int SEQ_LEN, float* O,
+                          hipStream_t stream);
+
+/* NUM_QUERIES (<= 160) queries of ONE sequence, query i attending to the
+ * first SEQ_LENS[i] tokens; Q/O [NUM_QUERIES,NH,HD].  Replaces
+ * jac_launch_batched, crates/jac-codegen-cuda/src/variants.rs:2776-2930
+ * (declared at source_patch.py:608-614). */
+void jac_launch_batched(const jacq_half_t* Q, const int32_t* SEQ_LENS,
+                        const int32_t* BLOCK_TABLE, const uint8_t* K_CODE_PAGES,
+                        const jacq_half_t* K_SCALE_PAGES, const jacq_half_t* K_ZERO_PAGES,
+                        const uint8_t* V_CODE_PAGES, const jacq_half_t* V_SCALE_PAGES,
+                        const jacq_half_t* V_ZERO_PAGES, const jacq_half_t* K_RESIDUAL_SCRATCH,
+                        const jacq_half_t* V_RESIDUAL_SCRATCH, int NUM_QUERIES, float* O,
+                        hipStream_t stream);
+
+/* source_patch.py:616-622. */
+void jac_launch_batched_tp2_local(const jacq_half_t* Q, const int32_t* SEQ_LENS,
+                                  const int32_t* BLOCK_TABLE, const uint8_t* K_CODE_PAGES,
+                                  const jacq_half_t* K_SCALE_PAGES,
+                                  const jacq_half_t* K_ZERO_PAGES, const uint8_t* V_CODE_PAGES,
+                                  const jacq_half_t* V_SCALE_PAGES,
+                                  const jacq_half_t* V_ZERO_PAGES,
+                                  const jacq_half_t* K_RESIDUAL_SCRATCH,
+                                  const jacq_half_t* V_RESIDUAL_SCRATCH, int NUM_QUERIES,
+                                  float* O, hipStream_t stream);
+
+/* Single-token cache write (NEW_K/NEW_V [NKV,HD]); SEQ_LEN is the length
+ * after the append.  Replaces jac_launch_cache_write, variants.rs:3226-3253
+ * (declared at source_patch.py:643-648). */
+void jac_launch_cache_write(uint8_t* K_CODE_PAGES, jacq_half_t* K_SCALE_PAGES,
+                            jacq_half_t* K_ZERO_PAGES, uint8_t* V_CODE_PAGES,
+                            jacq_half_t* V_SCALE_PAGES, jacq_half_t* V_ZERO_PAGES,
+                            jacq_half_t* K_RESIDUAL_SCRATCH, jacq_half_t* V_RESIDUAL_SCRATCH,
+                            const jacq_half_t* NEW_K, const jacq_half_t* NEW_V,
+                            const int32_t* BLOCK_TABLE, int SEQ_LEN, hipStream_t stream);
+
+/* NUM_NEW (<= 160) token-major tokens [NUM_NEW,NKV,HD] appended at
+ * START_SEQ_LEN.  Replaces jac_launch_cache_write_batched,
+ * variants.rs:3186-3268 (declared at source_patch.py:653-658). */
+void jac_launch_cache_write_batched(uint8_t* K_CODE_PAGES, jacq_half_t* K_SCALE_PAGES,
+                                    jacq_half_t* K_ZERO_PAGES, uint8_t* V_CODE_PAGES,
+                                    jacq_half_t* V_SCALE_PAGES, jacq_half_t* V_ZERO_PAGES,
+                                    jacq_half_t* K_RESIDUAL_SCRATCH,
+                                    jacq_half_t* V_RESIDUAL_SCRATCH, const jacq_half_t* NEW_K,
+                                    const jacq_half_t* NEW_V, const int32_t* BLOCK_TABLE,
+                                    int START_SEQ_LEN, int NUM_NEW, hipStream_t stream);
+
+/* The hand-written writer's host entry, source_patch.py:624-629 / :1661-1697.
+ * SLOT_MAPPING is accepted and ignored, as in the reference (:1667-1675).
+ * NKV_RUNTIME selects 8 (global) or 4 (TP=2 local).  The reference declares
+ * this with C++ linkage; here it has C linkage. */
+void kivi_cache_write_launch(uint8_t* K_CODE_PAGES, jacq_half_t* K_SCALE_PAGES,
+                             jacq_half_t* K_ZERO_PAGES, uint8_t* V_CODE_PAGES,
+                             jacq_half_t* V_SCALE_PAGES, jacq_half_t* V_ZERO_PAGES,
+                             jacq_half_t* K_RESIDUAL_SCRATCH, jacq_half_t* V_RESIDUAL_SCRATCH,
+                             const jacq_half_t* NEW_K, const jacq_half_t* NEW_V,
+                             const int64_t* SLOT_MAPPING, const int32_t* BLOCK_TABLE,
+                             int seq_len, int NKV_RUNTIME, hipStream_t stream);
+
+/* source_patch.py:631-637 / :1737-1775. */
+void kivi_cache_write_batched_launch(uint8_t* K_CODE_PAGES, jacq_half_t* K_SCALE_PAGES,
+                                     jacq_half_t* K_ZERO_PAGES, uint8_t* V_CODE_PAGES,
+                                     jacq_half_t* V_SCALE_PAGES, jacq_half_t* V_ZERO_PAGES,
+                                     jacq_half_t* K_RESIDUAL_SCRATCH,
+                                     jacq_half_t* V_RESIDUAL_SCRATCH, const jacq_half_t* NEW_K,
+                                     const jacq_half_t* NEW_V, const int64_t* SLOT_MAPPING,
+                                     const int32_t* BLOCK_TABLE, int START_SEQ_LEN, int NUM_NEW,
+                                     int NKV_RUNTIME, hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* 2. Runtime-geometry surface                                               */
+/* ------------------------------------------------------------------------ */
+
+/* Status codes of the jacq_kivi_* functions. */
+#define JACQ_KIVI_OK 0
+#define JACQ_KIVI_EINVAL 1   /* argument outside the supported contract */
+#define JACQ_KIVI_EHIP 2     /* a HIP runtime call failed */
+#define JACQ_KIVI_ENOMEM 3   /* workspace allocation failed / too small */
+
+typedef struct jacq_kivi_geometry {
+  int32_t num_heads;         /* NH */
+  int32_t num_kv_heads;      /* NKV; NH % NKV == 0, NH / NKV <= 16 */
+  int32_t head_dim;          /* HD: 64 or 128 */
+  int32_t page_size;         /* P: 16 or 32 tokens per physical page */
+  int32_t group_size;        /* quantisation group: 32 */
+  int32_t residual;          /* R: fp16 window, positive multiple of 32 */
+  int32_t max_pages_per_seq; /* block-table row width */
+  int32_t num_pages;         /* physical pages in the pool */
+} jacq_kivi_geometry;
+
+/* ABI v1 contract version (1) and runtime-geometry surface version. */
+int jacq_kivi_abi_version(void);
+int jacq_kivi_ext_version(void);
+
+/* Message of the last error reported by a jacq_kivi_* call on this thread. */
+const char* jacq_kivi_last_error(void);
+
+/* Geometry check (integrations/vllm_kivi/layout.py:51-74 and the supported
+ * geometry checks of source_patch.py:744-756, generalised). */
+int jacq_kivi_check_geometry(const jacq_kivi_geometry* geo);
+
+/* Longest sequence the geometry addresses: old-token capacity of the table
+ * (whole groups) + R.  4096 for the v1 geometry (abi.py:48-53). */
+int64_t jacq_kivi_max_seq_len(const jacq_kivi_geometry* geo);
+
+/* check_block_table_width, source_patch.py:692-707, at runtime geometry:
+ * JACQ_KIVI_OK when a table of `width` entries covers a sequence of
+ * `seq_len` tokens, JACQ_KIVI_EINVAL otherwise (message names the bound). */
+int jacq_kivi_check_block_table_width(const jacq_kivi_geometry* geo, int64_t width,
+                                      int64_t seq_len);
+
+/* Bytes of split-K workspace jacq_kivi_decode needs for `batch` sequences. */
+size_t jacq_kivi_decode_workspace_size(const jacq_kivi_geometry* geo, int32_t batch);
+
+/* Decode one query token per sequence for `batch` sequences.
+ *   Q             [batch, NH, HD] fp16
+ *   SEQ_LENS      [batch] int32 (device), tokens each query attends to
+ *   BLOCK_TABLES  [batch, max_pages_per_seq] int32
+ *   K/V_SCR       [batch, NKV, R+32, HD] fp16
+ *   O             [batch, NH, HD] fp32
+ * workspace may be NULL (the library then uses its own, allocated once per
+ * device and grown on demand) or at least jacq_kivi_decode_workspace_size
+ * bytes.  Sequence lengths are clamped to [0, jacq_kivi_max_seq_len] on the
+ * device, as the reference kernel clamps (snapshot :74-83). */
+int jacq_kivi_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q,
+                     const int32_t* SEQ_LENS, const int32_t* BLOCK_TABLES,
+                     const uint8_t* K_CODE_PAGES, const jacq_half_t* K_SCALE_PAGES,
+                     const jacq_half_t* K_ZERO_PAGES, const uint8_t* V_CODE_PAGES,
+                     const jacq_half_t* V_SCALE_PAGES, const jacq_half_t* V_ZERO_PAGES,
+                     const jacq_half_t* K_RESIDUAL_SCRATCH,
+                     const jacq_half_t* V_RESIDUAL_SCRATCH, int32_t batch, float* O,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Append num_new tokens to each of `batch` sequences in one launch.
+ *   NEW_K/NEW_V   [batch, num_new, NKV, HD] fp16, token-major per sequence
+ *   START_LENS    [batch] int32 (device), length of each sequence before
+ *                 the append
+ * Any num_new >= 1: every group that ages out is quantised (bit-identical to
+ * feeding the tokens one at a time through jac_launch_cache_write) and the
+ * residual scratch ends holding the newest tokens.  When
+ * residual_len + num_new <= R + 32 (at most one age-out) the scratch goes
+ * through exactly the reference's append-then-shift states; otherwise only
+ * its first residual_len rows are defined. */
+int jacq_kivi_cache_append(const jacq_kivi_geometry* geo, uint8_t* K_CODE_PAGES,
+                           jacq_half_t* K_SCALE_PAGES, jacq_half_t* K_ZERO_PAGES,
+                           uint8_t* V_CODE_PAGES, jacq_half_t* V_SCALE_PAGES,
+                           jacq_half_t* V_ZERO_PAGES, jacq_half_t* K_RESIDUAL_SCRATCH,
+                           jacq_half_t* V_RESIDUAL_SCRATCH, const jacq_half_t* NEW_K,
+                           const jacq_half_t* NEW_V, const int32_t* BLOCK_TABLES,
+                           const int32_t* START_LENS, int32_t num_new, int32_t batch,
+                           hipStream_t stream);
+
+/* One entry of the batched-write plan, source_patch.py:495-501.
+ * age_out_page / post_shift_residual_len are -1 for None. */
+typedef struct jacq_kivi_subchunk {
+  int32_t start_seq_len;
+  int32_t num_new;
+  int32_t scratch_start;
+  int32_t age_out_page;
+  int32_t post_shift_residual_len;
+} jacq_kivi_subchunk;
+
+/* plan_batched_write, source_patch.py:504-553 (host only).  Returns the
+ * number of sub-chunks written to `out` (at most `cap`), or -1 with
+ * jacq_kivi_last_error() set (the reference raises ValueError). */
+int32_t jacq_kivi_plan_batched_write(int32_t start_seq_len, int32_t num_new, int32_t residual,
+                                     int32_t group, jacq_kivi_subchunk* out, int32_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JACQ_KIVI_H */

@@ -1,0 +1,10 @@
+"""jacq_amd -- MI355X (gfx950) implementation of Jacq's int4-KIVI paged
+KV-cache hot path: the cache writer and paged decode attention, behind the
+reference's callable C launch contract (include/jacq_kivi.h).
+
+The native library is ``jacq_amd/libjacq_kivi.so`` (``python -m jacq_amd.build``).
+``jacq_amd.kivi`` binds it; there is no CPU fallback.
+"""
+from jacq_amd import abi, bindings, layout  # noqa: F401
+
+__all__ = ["abi", "bindings", "layout", "kivi", "workloads"]

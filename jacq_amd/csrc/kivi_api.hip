@@ -1,0 +1,493 @@
+// kivi_api.hip -- host side of libjacq_kivi.so: the C ABI of include/jacq_kivi.h.
+//
+// The v1 symbols keep the reference's launch contract (fixed geometry per
+// symbol, void return, launch errors reported on stderr followed by exit(1)
+// as the emitted CUDA_CHECK does, decode_attention_kivi_paged_library_flash.cu:9-12,
+// :171).  The jacq_kivi_* symbols validate their arguments and return a
+// status code; jacq_kivi_last_error() holds the message.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdio>
+#include <cstdlib>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "jacq_kivi.h"
+#include "kivi_kernels.h"
+
+namespace {
+
+using jacq::KiviGeo;
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+// Reference geometries: source_patch.py:660-671 (NH/NKV/TP2 local, HD,
+// OLD_BLOCKS, BLOCK_SIZE, RESIDUAL).
+constexpr jacq_kivi_geometry kGlobal = {40, 8, 128, 32, 32, 128, 124, INT32_MAX};
+constexpr jacq_kivi_geometry kTp2Local = {20, 4, 128, 32, 32, 128, 124, INT32_MAX};
+
+int check_geometry(const jacq_kivi_geometry* x) {
+  if (!x) return fail(JACQ_KIVI_EINVAL, "geometry pointer is null");
+  if (x->num_heads < 1 || x->num_kv_heads < 1 || x->num_heads % x->num_kv_heads != 0)
+    return fail(JACQ_KIVI_EINVAL, "num_heads must be a positive multiple of num_kv_heads, got " +
+                                      std::to_string(x->num_heads) + "/" +
+                                      std::to_string(x->num_kv_heads));
+  if (x->num_heads / x->num_kv_heads > 16)
+    return fail(JACQ_KIVI_EINVAL, "query heads per kv head must be <= 16");
+  if (x->head_dim != 64 && x->head_dim != 128)
+    return fail(JACQ_KIVI_EINVAL, "head_dim must be 64 or 128, got " + std::to_string(x->head_dim));
+  if (x->group_size != jacq::kGroup)
+    return fail(JACQ_KIVI_EINVAL, "group_size must be 32 (int4 KIVI lane), got " +
+                                      std::to_string(x->group_size));
+  if (x->page_size != 16 && x->page_size != 32)
+    return fail(JACQ_KIVI_EINVAL, "page_size must be 16 or 32 (a divisor of the 32-token group), got " +
+                                      std::to_string(x->page_size));
+  if (x->residual <= 0 || x->residual % x->group_size != 0)
+    return fail(JACQ_KIVI_EINVAL, "residual must be a positive multiple of the group, got " +
+                                      std::to_string(x->residual));
+  if (x->max_pages_per_seq < 0) return fail(JACQ_KIVI_EINVAL, "max_pages_per_seq must be >= 0");
+  if (x->num_pages < 1)
+    return fail(JACQ_KIVI_EINVAL, "num_pages (page storage capacity) must be positive");
+  return JACQ_KIVI_OK;
+}
+
+KiviGeo make_geo(const jacq_kivi_geometry& x) {
+  KiviGeo g;
+  g.nh = x.num_heads;
+  g.nkv = x.num_kv_heads;
+  g.hd = x.head_dim;
+  g.page = x.page_size;
+  g.residual = x.residual;
+  g.max_pages = x.max_pages_per_seq;
+  g.num_pages = x.num_pages;
+  g.gqa = x.num_heads / x.num_kv_heads;
+  g.rs = x.residual + jacq::kGroup;
+  g.lq = (int)(((int64_t)x.max_pages_per_seq * x.page_size / jacq::kGroup) * jacq::kGroup);
+  return g;
+}
+
+int64_t max_seq_len(const jacq_kivi_geometry& x) {
+  return ((int64_t)x.max_pages_per_seq * x.page_size / jacq::kGroup) * jacq::kGroup + x.residual;
+}
+
+// ---- device properties and the library-owned split-K workspace ----
+
+struct DeviceState {
+  int cus = 0;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+};
+std::mutex g_mu;
+std::vector<DeviceState> g_dev;
+
+int current_device(int* dev) {
+  if (hipGetDevice(dev) != hipSuccess) return fail(JACQ_KIVI_EHIP, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lk(g_mu);
+  if ((int)g_dev.size() <= *dev) g_dev.resize(*dev + 1);
+  if (g_dev[*dev].cus == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, *dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    g_dev[*dev].cus = cus;
+  }
+  return JACQ_KIVI_OK;
+}
+
+int library_workspace(int dev, size_t bytes, void** out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceState& s = g_dev[dev];
+  if (s.ws_bytes < bytes) {
+    if (s.ws) {
+      // hipFree waits for work that may still read the old buffer.
+      if (hipFree(s.ws) != hipSuccess) return fail(JACQ_KIVI_EHIP, "hipFree(workspace) failed");
+      s.ws = nullptr;
+      s.ws_bytes = 0;
+    }
+    const size_t want = bytes + bytes / 4;
+    if (hipMalloc(&s.ws, want) != hipSuccess) {
+      s.ws = nullptr;
+      return fail(JACQ_KIVI_ENOMEM, "hipMalloc of " + std::to_string(want) +
+                                         " workspace bytes failed");
+    }
+    s.ws_bytes = want;
+  }
+  *out = s.ws;
+  return JACQ_KIVI_OK;
+}
+
+// Split slots per (sequence, kv head): split_plan never makes more than
+// min(kMaxSplits, ceil(n / kSplitTarget)) splits, which grows with n, so the
+// longest sequence the call can see bounds every sequence's count.
+struct SplitPlan {
+  int max_splits;
+};
+
+SplitPlan plan_splits(int64_t max_tokens) {
+  int64_t s = (max_tokens + jacq::kSplitTarget - 1) / jacq::kSplitTarget;
+  if (s < 1) s = 1;
+  if (s > jacq::kMaxSplits) s = jacq::kMaxSplits;
+  return {(int)s};
+}
+
+size_t workspace_bytes(const KiviGeo& g, int batch, const SplitPlan& sp) {
+  if (sp.max_splits <= 1) return 0;
+  const size_t slots = (size_t)batch * g.nkv * sp.max_splits * g.gqa;
+  return slots * (size_t)(g.hd + 2) * sizeof(float) + 256;
+}
+
+void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& sp, void* ws) {
+  a.max_splits = sp.max_splits;
+  const size_t slots = (size_t)batch * g.nkv * sp.max_splits * g.gqa;
+  a.ws_acc = (float*)ws;
+  a.ws_ml = ws ? (float*)ws + slots * g.hd : nullptr;
+}
+
+// Decode with a runtime geometry; seq_len_host >= 0 when the (single) length
+// is known on the host, which tightens the split plan.
+int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t* seq_lens,
+               int seq_len_host, const int32_t* bt, int64_t bt_stride, const uint8_t* kc,
+               const jacq_half_t* ksc, const jacq_half_t* kz, const uint8_t* vc,
+               const jacq_half_t* vsc, const jacq_half_t* vz, const jacq_half_t* kscr,
+               const jacq_half_t* vscr, int64_t scr_stride, int batch, float* O, void* ws,
+               size_t ws_bytes, hipStream_t stream) {
+  const KiviGeo g = make_geo(x);
+  int dev = 0;
+  if (int e = current_device(&dev)) return e;
+  int64_t max_tokens = max_seq_len(x);
+  if (seq_len_host >= 0) {
+    int ov, rv;
+    jacq::decode_window(g, seq_len_host, &ov, &rv);
+    max_tokens = ov + rv;
+  }
+  const SplitPlan sp = plan_splits(max_tokens);
+  const size_t need = workspace_bytes(g, batch, sp);
+  if (need > 0) {
+    if (ws == nullptr) {
+      if (int e = library_workspace(dev, need, &ws)) return e;
+    } else if (ws_bytes < need) {
+      return fail(JACQ_KIVI_ENOMEM, "workspace of " + std::to_string(ws_bytes) +
+                                         " bytes is smaller than the " + std::to_string(need) +
+                                         " required");
+    }
+  }
+  jacq::DecodeArgs a{};
+  a.q = Q;
+  a.q_stride = (int64_t)g.nh * g.hd;
+  a.seq_lens = seq_lens;
+  a.seq_len = seq_len_host;
+  a.block_tables = bt;
+  a.bt_stride = bt_stride;
+  a.k_code = kc;
+  a.k_scale = ksc;
+  a.k_zero = kz;
+  a.v_code = vc;
+  a.v_scale = vsc;
+  a.v_zero = vz;
+  a.k_scr = kscr;
+  a.v_scr = vscr;
+  a.scr_stride = scr_stride;
+  a.out = O;
+  a.out_stride = (int64_t)g.nh * g.hd;
+  fill_ws(a, g, batch, sp, need > 0 ? ws : nullptr);
+  if (jacq::launch_decode(g, a, batch, stream) != hipSuccess)
+    return fail(JACQ_KIVI_EHIP, "decode launch failed");
+  return JACQ_KIVI_OK;
+}
+
+int run_append(const jacq_kivi_geometry& x, uint8_t* kc, jacq_half_t* ksc, jacq_half_t* kz,
+               uint8_t* vc, jacq_half_t* vsc, jacq_half_t* vz, jacq_half_t* kscr,
+               jacq_half_t* vscr, int64_t scr_stride, const jacq_half_t* nk,
+               const jacq_half_t* nv, int64_t new_stride, const int32_t* bt, int64_t bt_stride,
+               const int32_t* start_lens, int start_len, int num_new, int batch,
+               hipStream_t stream) {
+  const KiviGeo g = make_geo(x);
+  jacq::AppendArgs a{};
+  a.k_code = kc;
+  a.k_scale = ksc;
+  a.k_zero = kz;
+  a.v_code = vc;
+  a.v_scale = vsc;
+  a.v_zero = vz;
+  a.k_scr = kscr;
+  a.v_scr = vscr;
+  a.scr_stride = scr_stride;
+  a.new_k = nk;
+  a.new_v = nv;
+  a.new_stride = new_stride;
+  a.block_tables = bt;
+  a.bt_stride = bt_stride;
+  a.start_lens = start_lens;
+  a.start_len = start_len;
+  a.num_new = num_new;
+  if (jacq::launch_append(g, a, batch, stream) != hipSuccess)
+    return fail(JACQ_KIVI_EHIP, "cache-write launch failed");
+  return JACQ_KIVI_OK;
+}
+
+// CUDA_CHECK of the emitted v1 symbols: report and exit(1).
+void v1_check(int status, const char* where) {
+  if (status == JACQ_KIVI_OK) return;
+  const hipError_t e = hipGetLastError();
+  std::fprintf(stderr, "HIP error %s in %s: %s\n", hipGetErrorString(e), where,
+               g_last_error.c_str());
+  std::exit(1);
+}
+
+}  // namespace
+
+extern "C" {
+
+int jacq_kivi_abi_version(void) { return JACQ_KIVI_ABI_VERSION; }
+int jacq_kivi_ext_version(void) { return JACQ_KIVI_EXT_VERSION; }
+const char* jacq_kivi_last_error(void) { return g_last_error.c_str(); }
+
+int jacq_kivi_check_geometry(const jacq_kivi_geometry* geo) { return check_geometry(geo); }
+
+int64_t jacq_kivi_max_seq_len(const jacq_kivi_geometry* geo) {
+  if (check_geometry(geo) != JACQ_KIVI_OK) return -1;
+  return max_seq_len(*geo);
+}
+
+int jacq_kivi_check_block_table_width(const jacq_kivi_geometry* geo, int64_t width,
+                                      int64_t seq_len) {
+  if (int e = check_geometry(geo)) return e;
+  const int64_t cap = max_seq_len(*geo);
+  if (seq_len < 1 || seq_len > cap)
+    return fail(JACQ_KIVI_EINVAL, "SEQ_LEN must be in [1, " + std::to_string(cap) +
+                                      "] for KIVI BLOCK_TABLE validation");
+  const int64_t required =
+      seq_len > geo->residual
+          ? ((seq_len - geo->residual) / geo->group_size) * geo->group_size / geo->page_size
+          : 0;
+  if (width < required)
+    return fail(JACQ_KIVI_EINVAL, "BLOCK_TABLE dim 0 must be at least " + std::to_string(required) +
+                                      ", got " + std::to_string(width));
+  return JACQ_KIVI_OK;
+}
+
+size_t jacq_kivi_decode_workspace_size(const jacq_kivi_geometry* geo, int32_t batch) {
+  if (check_geometry(geo) != JACQ_KIVI_OK || batch < 1) return 0;
+  int dev = 0;
+  if (current_device(&dev) != JACQ_KIVI_OK) return 0;
+  const KiviGeo g = make_geo(*geo);
+  return workspace_bytes(g, batch, plan_splits(max_seq_len(*geo)));
+}
+
+int jacq_kivi_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q, const int32_t* SEQ_LENS,
+                     const int32_t* BLOCK_TABLES, const uint8_t* K_CODE_PAGES,
+                     const jacq_half_t* K_SCALE_PAGES, const jacq_half_t* K_ZERO_PAGES,
+                     const uint8_t* V_CODE_PAGES, const jacq_half_t* V_SCALE_PAGES,
+                     const jacq_half_t* V_ZERO_PAGES, const jacq_half_t* K_RESIDUAL_SCRATCH,
+                     const jacq_half_t* V_RESIDUAL_SCRATCH, int32_t batch, float* O,
+                     void* workspace, size_t workspace_bytes_, hipStream_t stream) {
+  if (int e = check_geometry(geo)) return e;
+  if (batch < 1) return fail(JACQ_KIVI_EINVAL, "batch must be >= 1");
+  if (!Q || !SEQ_LENS || !K_CODE_PAGES || !K_SCALE_PAGES || !K_ZERO_PAGES || !V_CODE_PAGES ||
+      !V_SCALE_PAGES || !V_ZERO_PAGES || !K_RESIDUAL_SCRATCH || !V_RESIDUAL_SCRATCH || !O ||
+      (!BLOCK_TABLES && geo->max_pages_per_seq > 0))
+    return fail(JACQ_KIVI_EINVAL, "null tensor pointer");
+  const int64_t scr = (int64_t)geo->num_kv_heads * (geo->residual + geo->group_size) * geo->head_dim;
+  return run_decode(*geo, Q, SEQ_LENS, -1, BLOCK_TABLES, geo->max_pages_per_seq, K_CODE_PAGES,
+                    K_SCALE_PAGES, K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES,
+                    K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, scr, batch, O, workspace,
+                    workspace_bytes_, stream);
+}
+
+int jacq_kivi_cache_append(const jacq_kivi_geometry* geo, uint8_t* K_CODE_PAGES,
+                           jacq_half_t* K_SCALE_PAGES, jacq_half_t* K_ZERO_PAGES,
+                           uint8_t* V_CODE_PAGES, jacq_half_t* V_SCALE_PAGES,
+                           jacq_half_t* V_ZERO_PAGES, jacq_half_t* K_RESIDUAL_SCRATCH,
+                           jacq_half_t* V_RESIDUAL_SCRATCH, const jacq_half_t* NEW_K,
+                           const jacq_half_t* NEW_V, const int32_t* BLOCK_TABLES,
+                           const int32_t* START_LENS, int32_t num_new, int32_t batch,
+                           hipStream_t stream) {
+  if (int e = check_geometry(geo)) return e;
+  if (batch < 1) return fail(JACQ_KIVI_EINVAL, "batch must be >= 1");
+  if (num_new < 1) return fail(JACQ_KIVI_EINVAL, "num_new must be >= 1");
+  if (!K_CODE_PAGES || !K_SCALE_PAGES || !K_ZERO_PAGES || !V_CODE_PAGES || !V_SCALE_PAGES ||
+      !V_ZERO_PAGES || !K_RESIDUAL_SCRATCH || !V_RESIDUAL_SCRATCH || !NEW_K || !NEW_V ||
+      !START_LENS || (!BLOCK_TABLES && geo->max_pages_per_seq > 0))
+    return fail(JACQ_KIVI_EINVAL, "null tensor pointer");
+  const int64_t scr = (int64_t)geo->num_kv_heads * (geo->residual + geo->group_size) * geo->head_dim;
+  const int64_t nst = (int64_t)num_new * geo->num_kv_heads * geo->head_dim;
+  return run_append(*geo, K_CODE_PAGES, K_SCALE_PAGES, K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES,
+                    V_ZERO_PAGES, K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, scr, NEW_K, NEW_V, nst,
+                    BLOCK_TABLES, geo->max_pages_per_seq, START_LENS, 0, num_new, batch, stream);
+}
+
+// plan_batched_write, source_patch.py:504-553.
+int32_t jacq_kivi_plan_batched_write(int32_t start_seq_len, int32_t num_new, int32_t residual,
+                                     int32_t group, jacq_kivi_subchunk* out, int32_t cap) {
+  if (start_seq_len < 0)
+    return fail(-1, "start_seq_len must be >= 0, got " + std::to_string(start_seq_len));
+  if (num_new < 1) return fail(-1, "num_new_tokens must be >= 1, got " + std::to_string(num_new));
+  if (residual <= 0 || group <= 0) return fail(-1, "residual and block_size must be positive");
+  auto split = [&](int32_t L) {
+    const int32_t q = L - residual;
+    return q < 0 ? 0 : (q / group) * group;
+  };
+  const int32_t capacity = residual + group;
+  int32_t n = 0, seq_len = start_seq_len, remaining = num_new;
+  while (remaining > 0) {
+    const int32_t prev_old = split(seq_len);
+    const int32_t prev_res = seq_len - prev_old;
+    const int32_t room = capacity - prev_res;
+    const int32_t take = remaining < room ? remaining : room;
+    if (take <= 0)
+      return fail(-1, "planning invariant violated: no room to append even one token "
+                      "(prev_residual_len=" + std::to_string(prev_res) +
+                      ", scratch_capacity=" + std::to_string(capacity) + ")");
+    const int32_t new_len = seq_len + take;
+    const int32_t next_old = split(new_len);
+    if (n >= cap) return fail(-1, "sub-chunk buffer too small");
+    out[n].start_seq_len = seq_len;
+    out[n].num_new = take;
+    out[n].scratch_start = prev_res;
+    out[n].age_out_page = next_old > prev_old ? prev_old / group : -1;
+    out[n].post_shift_residual_len = next_old > prev_old ? new_len - next_old : -1;
+    ++n;
+    seq_len = new_len;
+    remaining -= take;
+  }
+  return n;
+}
+
+// ---- reference contract, ABI v1 ----
+
+void jac_launch(const jacq_half_t* Q, const int32_t* BLOCK_TABLE, const uint8_t* K_CODE_PAGES,
+                const jacq_half_t* K_SCALE_PAGES, const jacq_half_t* K_ZERO_PAGES,
+                const uint8_t* V_CODE_PAGES, const jacq_half_t* V_SCALE_PAGES,
+                const jacq_half_t* V_ZERO_PAGES, const jacq_half_t* K_RESIDUAL_SCRATCH,
+                const jacq_half_t* V_RESIDUAL_SCRATCH, int SEQ_LEN, float* O,
+                hipStream_t stream) {
+  v1_check(run_decode(kGlobal, Q, nullptr, SEQ_LEN, BLOCK_TABLE, 0, K_CODE_PAGES, K_SCALE_PAGES,
+                      K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES,
+                      K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, 0, 1, O, nullptr, 0, stream),
+           "jac_launch");
+}
+
+void jac_launch_tp2_local(const jacq_half_t* Q, const int32_t* BLOCK_TABLE,
+                          const uint8_t* K_CODE_PAGES, const jacq_half_t* K_SCALE_PAGES,
+                          const jacq_half_t* K_ZERO_PAGES, const uint8_t* V_CODE_PAGES,
+                          const jacq_half_t* V_SCALE_PAGES, const jacq_half_t* V_ZERO_PAGES,
+                          const jacq_half_t* K_RESIDUAL_SCRATCH,
+                          const jacq_half_t* V_RESIDUAL_SCRATCH, int SEQ_LEN, float* O,
+                          hipStream_t stream) {
+  v1_check(run_decode(kTp2Local, Q, nullptr, SEQ_LEN, BLOCK_TABLE, 0, K_CODE_PAGES,
+                      K_SCALE_PAGES, K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES,
+                      K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, 0, 1, O, nullptr, 0, stream),
+           "jac_launch_tp2_local");
+}
+
+static void batched_v1(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t* SEQ_LENS,
+                       const int32_t* BLOCK_TABLE, const uint8_t* kc, const jacq_half_t* ks,
+                       const jacq_half_t* kz, const uint8_t* vc, const jacq_half_t* vs,
+                       const jacq_half_t* vz, const jacq_half_t* kscr, const jacq_half_t* vscr,
+                       int NUM_QUERIES, float* O, hipStream_t stream, const char* where) {
+  if (NUM_QUERIES < 1) return;  // an empty grid: the reference launch would be a no-op error
+  v1_check(run_decode(x, Q, SEQ_LENS, -1, BLOCK_TABLE, 0, kc, ks, kz, vc, vs, vz, kscr, vscr, 0,
+                      NUM_QUERIES, O, nullptr, 0, stream),
+           where);
+}
+
+void jac_launch_batched(const jacq_half_t* Q, const int32_t* SEQ_LENS, const int32_t* BLOCK_TABLE,
+                        const uint8_t* K_CODE_PAGES, const jacq_half_t* K_SCALE_PAGES,
+                        const jacq_half_t* K_ZERO_PAGES, const uint8_t* V_CODE_PAGES,
+                        const jacq_half_t* V_SCALE_PAGES, const jacq_half_t* V_ZERO_PAGES,
+                        const jacq_half_t* K_RESIDUAL_SCRATCH,
+                        const jacq_half_t* V_RESIDUAL_SCRATCH, int NUM_QUERIES, float* O,
+                        hipStream_t stream) {
+  batched_v1(kGlobal, Q, SEQ_LENS, BLOCK_TABLE, K_CODE_PAGES, K_SCALE_PAGES, K_ZERO_PAGES,
+             V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES, K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH,
+             NUM_QUERIES, O, stream, "jac_launch_batched");
+}
+
+void jac_launch_batched_tp2_local(const jacq_half_t* Q, const int32_t* SEQ_LENS,
+                                  const int32_t* BLOCK_TABLE, const uint8_t* K_CODE_PAGES,
+                                  const jacq_half_t* K_SCALE_PAGES,
+                                  const jacq_half_t* K_ZERO_PAGES, const uint8_t* V_CODE_PAGES,
+                                  const jacq_half_t* V_SCALE_PAGES,
+                                  const jacq_half_t* V_ZERO_PAGES,
+                                  const jacq_half_t* K_RESIDUAL_SCRATCH,
+                                  const jacq_half_t* V_RESIDUAL_SCRATCH, int NUM_QUERIES,
+                                  float* O, hipStream_t stream) {
+  batched_v1(kTp2Local, Q, SEQ_LENS, BLOCK_TABLE, K_CODE_PAGES, K_SCALE_PAGES, K_ZERO_PAGES,
+             V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES, K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH,
+             NUM_QUERIES, O, stream, "jac_launch_batched_tp2_local");
+}
+
+static jacq_kivi_geometry writer_geo(int nkv) {
+  jacq_kivi_geometry x = kGlobal;
+  x.num_kv_heads = nkv;
+  x.num_heads = nkv * (kGlobal.num_heads / kGlobal.num_kv_heads);
+  return x;
+}
+
+void jac_launch_cache_write(uint8_t* K_CODE_PAGES, jacq_half_t* K_SCALE_PAGES,
+                            jacq_half_t* K_ZERO_PAGES, uint8_t* V_CODE_PAGES,
+                            jacq_half_t* V_SCALE_PAGES, jacq_half_t* V_ZERO_PAGES,
+                            jacq_half_t* K_RESIDUAL_SCRATCH, jacq_half_t* V_RESIDUAL_SCRATCH,
+                            const jacq_half_t* NEW_K, const jacq_half_t* NEW_V,
+                            const int32_t* BLOCK_TABLE, int SEQ_LEN, hipStream_t stream) {
+  v1_check(run_append(kGlobal, K_CODE_PAGES, K_SCALE_PAGES, K_ZERO_PAGES, V_CODE_PAGES,
+                      V_SCALE_PAGES, V_ZERO_PAGES, K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, 0,
+                      NEW_K, NEW_V, 0, BLOCK_TABLE, 0, nullptr, SEQ_LEN - 1, 1, 1, stream),
+           "jac_launch_cache_write");
+}
+
+void jac_launch_cache_write_batched(uint8_t* K_CODE_PAGES, jacq_half_t* K_SCALE_PAGES,
+                                    jacq_half_t* K_ZERO_PAGES, uint8_t* V_CODE_PAGES,
+                                    jacq_half_t* V_SCALE_PAGES, jacq_half_t* V_ZERO_PAGES,
+                                    jacq_half_t* K_RESIDUAL_SCRATCH,
+                                    jacq_half_t* V_RESIDUAL_SCRATCH, const jacq_half_t* NEW_K,
+                                    const jacq_half_t* NEW_V, const int32_t* BLOCK_TABLE,
+                                    int START_SEQ_LEN, int NUM_NEW, hipStream_t stream) {
+  if (NUM_NEW < 1) return;
+  v1_check(run_append(kGlobal, K_CODE_PAGES, K_SCALE_PAGES, K_ZERO_PAGES, V_CODE_PAGES,
+                      V_SCALE_PAGES, V_ZERO_PAGES, K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, 0,
+                      NEW_K, NEW_V, 0, BLOCK_TABLE, 0, nullptr, START_SEQ_LEN, NUM_NEW, 1, stream),
+           "jac_launch_cache_write_batched");
+}
+
+void kivi_cache_write_launch(uint8_t* K_CODE_PAGES, jacq_half_t* K_SCALE_PAGES,
+                             jacq_half_t* K_ZERO_PAGES, uint8_t* V_CODE_PAGES,
+                             jacq_half_t* V_SCALE_PAGES, jacq_half_t* V_ZERO_PAGES,
+                             jacq_half_t* K_RESIDUAL_SCRATCH, jacq_half_t* V_RESIDUAL_SCRATCH,
+                             const jacq_half_t* NEW_K, const jacq_half_t* NEW_V,
+                             const int64_t* SLOT_MAPPING, const int32_t* BLOCK_TABLE, int seq_len,
+                             int NKV_RUNTIME, hipStream_t stream) {
+  (void)SLOT_MAPPING;  // placement comes from BLOCK_TABLE (source_patch.py:1667-1675)
+  if (NKV_RUNTIME < 1) return;
+  v1_check(run_append(writer_geo(NKV_RUNTIME), K_CODE_PAGES, K_SCALE_PAGES, K_ZERO_PAGES,
+                      V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES, K_RESIDUAL_SCRATCH,
+                      V_RESIDUAL_SCRATCH, 0, NEW_K, NEW_V, 0, BLOCK_TABLE, 0, nullptr, seq_len - 1,
+                      1, 1, stream),
+           "kivi_cache_write_launch");
+}
+
+void kivi_cache_write_batched_launch(uint8_t* K_CODE_PAGES, jacq_half_t* K_SCALE_PAGES,
+                                     jacq_half_t* K_ZERO_PAGES, uint8_t* V_CODE_PAGES,
+                                     jacq_half_t* V_SCALE_PAGES, jacq_half_t* V_ZERO_PAGES,
+                                     jacq_half_t* K_RESIDUAL_SCRATCH,
+                                     jacq_half_t* V_RESIDUAL_SCRATCH, const jacq_half_t* NEW_K,
+                                     const jacq_half_t* NEW_V, const int64_t* SLOT_MAPPING,
+                                     const int32_t* BLOCK_TABLE, int START_SEQ_LEN, int NUM_NEW,
+                                     int NKV_RUNTIME, hipStream_t stream) {
+  (void)SLOT_MAPPING;
+  if (NKV_RUNTIME < 1 || NUM_NEW < 1) return;
+  v1_check(run_append(writer_geo(NKV_RUNTIME), K_CODE_PAGES, K_SCALE_PAGES, K_ZERO_PAGES,
+                      V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES, K_RESIDUAL_SCRATCH,
+                      V_RESIDUAL_SCRATCH, 0, NEW_K, NEW_V, 0, BLOCK_TABLE, 0, nullptr,
+                      START_SEQ_LEN, NUM_NEW, 1, stream),
+           "kivi_cache_write_batched_launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,54 @@
+// kivi_kernels.h -- argument blocks and launchers of the gfx950 KIVI kernels.
+#pragma once
+
+#include "kivi_common.h"
+
+namespace jacq {
+
+struct AppendArgs {
+  uint8_t* k_code;
+  uint16_t* k_scale;
+  uint16_t* k_zero;
+  uint8_t* v_code;
+  uint16_t* v_scale;
+  uint16_t* v_zero;
+  uint16_t* k_scr;
+  uint16_t* v_scr;
+  int64_t scr_stride;  // elements between sequences' scratch (0: shared)
+  const uint16_t* new_k;
+  const uint16_t* new_v;
+  int64_t new_stride;  // elements between sequences' new tokens
+  const int32_t* block_tables;
+  int64_t bt_stride;          // entries between sequences' block-table rows
+  const int32_t* start_lens;  // device lengths before the append, or null
+  int start_len;              // used when start_lens is null
+  int num_new;
+};
+
+struct DecodeArgs {
+  const uint16_t* q;
+  int64_t q_stride;  // elements between queries (NH*HD)
+  const int32_t* seq_lens;  // device lengths, or null
+  int seq_len;              // used when seq_lens is null
+  const int32_t* block_tables;
+  int64_t bt_stride;  // 0: every query shares one table (jac_launch_batched)
+  const uint8_t* k_code;
+  const uint16_t* k_scale;
+  const uint16_t* k_zero;
+  const uint8_t* v_code;
+  const uint16_t* v_scale;
+  const uint16_t* v_zero;
+  const uint16_t* k_scr;
+  const uint16_t* v_scr;
+  int64_t scr_stride;  // 0: every query shares one scratch
+  float* out;
+  int64_t out_stride;
+  float* ws_ml;   // [batch, NKV, max_splits, G, 2]  (m, l)
+  float* ws_acc;  // [batch, NKV, max_splits, G, HD]
+  int max_splits;  // split slots per (sequence, kv head): grid.x and workspace stride
+};
+
+hipError_t launch_append(const KiviGeo& g, const AppendArgs& a, int batch, hipStream_t stream);
+hipError_t launch_decode(const KiviGeo& g, const DecodeArgs& a, int batch, hipStream_t stream);
+
+}  // namespace jacq

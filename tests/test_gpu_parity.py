@@ -1,0 +1,276 @@
+"""GPU parity: the HIP writer and decode through the C ABI versus the CPU oracle.
+
+Writer state (codes, scales, zeros, scratch) must be bit-exact; attention
+outputs within max-abs 2e-3 / rel 1e-2 of the float64 two-pass reference.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from jacq_amd import workloads as wl
+from oracle import oracle as o
+from tests.kivi_testlib import State, assert_close, to_torch
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+V1 = wl.Workload("v1", 40, 8, 128, 1, 4096, 4096, page=32, residual=128, outliers=8,
+                 outlier_scale=10.0, seed=11)
+
+
+@pytest.fixture(scope="module")
+def kivi():
+    from jacq_amd import kivi as k
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    k.lib()
+    return k
+
+
+def _np(t):
+    x = t.detach().cpu()
+    if x.dtype == torch.float16:
+        x = x.view(torch.int16)
+    return x.numpy().view(np.uint16) if x.dtype == torch.int16 else x.numpy()
+
+
+def _compare_pool(st: State, g: dict, scratch_rows=None, what=""):
+    c = st.cache
+    for name in ("k_code", "k_scale", "k_zero", "v_code", "v_scale", "v_zero"):
+        ref = getattr(c, name)
+        got = _np(g[name])
+        assert np.array_equal(got, ref), f"{what}: {name} differs at {np.argwhere(got != ref)[:5]}"
+    for name in ("k_scr", "v_scr"):
+        ref = getattr(c, name)
+        got = _np(g[name])
+        if scratch_rows is None:
+            assert np.array_equal(got, ref), f"{what}: {name} differs"
+        else:
+            for b, r in enumerate(scratch_rows):
+                assert np.array_equal(got[b, :, :r], ref[b, :, :r]), f"{what}: {name}[{b}] differs"
+
+
+# ---------------------------------------------------------------- writer
+
+def test_v1_single_token_writer_bit_exact(kivi):
+    """jac_launch_cache_write token by token through 3 age-outs: pages AND the
+    whole scratch (stale rows included) equal the reference's serial writer."""
+    st = State(V1, lens=[256], seed=5)
+    g = to_torch(st)
+    bt = torch.from_numpy(st.tables[0]).cuda()
+    for t in range(256):
+        nk = torch.from_numpy(st.k_hist[0][t].copy()).view(torch.float16).cuda()
+        nv = torch.from_numpy(st.v_hist[0][t].copy()).view(torch.float16).cuda()
+        kivi.lib().jac_launch_cache_write(
+            *[kivi._ptr(g[n]) for n in ("k_code", "k_scale", "k_zero", "v_code", "v_scale",
+                                        "v_zero")],
+            kivi._ptr(g["k_scr"][0]), kivi._ptr(g["v_scr"][0]), kivi._ptr(nk), kivi._ptr(nv),
+            kivi._ptr(bt), t + 1, kivi._stream(nk.device))
+        o.cache_write(st.cache, 0, st.k_hist[0][t], st.v_hist[0][t], st.tables[0], t + 1)
+        if (t + 1) in (159, 160, 161, 192, 224, 256):
+            torch.cuda.synchronize()
+            _compare_pool(st, g, what=f"after token {t + 1}")
+
+
+def test_torch_op_mirrors_write_then_decode(kivi):
+    """kivi_cache_write_dsl / kivi_decode_dsl (reference op surface) at the v1
+    geometry, global and TP=2 local."""
+    for nh, nkv in ((40, 8), (20, 4)):
+        w = wl.Workload("v1op", nh, nkv, 128, 1, 300, 300, page=32, residual=128, outliers=4,
+                        outlier_scale=10.0, seed=nh)
+        st = State(w, lens=[300])
+        g = to_torch(st)
+        bt = torch.from_numpy(st.tables[0]).cuda()
+        slot = torch.zeros(1, dtype=torch.int64, device="cuda")
+        pool = [g[n] for n in ("k_code", "k_scale", "k_zero", "v_code", "v_scale", "v_zero")]
+        for t in range(300):
+            nk = torch.from_numpy(st.k_hist[0][t].copy()).view(torch.float16).cuda()
+            nv = torch.from_numpy(st.v_hist[0][t].copy()).view(torch.float16).cuda()
+            kivi.kivi_cache_write_dsl(*pool, g["k_scr"][0], g["v_scr"][0], nk, nv, slot, bt, t + 1)
+        st.build_oracle()
+        torch.cuda.synchronize()
+        _compare_pool(st, g, what=f"op writer {nh}/{nkv}")
+        q = torch.from_numpy(st.q[0].copy()).view(torch.float16).cuda()
+        out = torch.empty((nh, 128), dtype=torch.float32, device="cuda")
+        kivi.kivi_decode_dsl(q, bt, *pool, g["k_scr"][0], g["v_scr"][0], 300, out)
+        torch.cuda.synchronize()
+        assert_close(out.cpu().numpy()[None], st.decode_ref(), f"kivi_decode_dsl {nh}/{nkv}")
+
+
+def test_batched_writer_matches_planned_single_writes(kivi):
+    """kivi_cache_write_batched_dsl over plan_batched_write sub-chunks of a
+    600-token prefill == the oracle's single-token writes."""
+    st = State(V1, lens=[600], seed=6)
+    g = to_torch(st)
+    bt = torch.from_numpy(st.tables[0]).cuda()
+    pool = [g[n] for n in ("k_code", "k_scale", "k_zero", "v_code", "v_scale", "v_zero")]
+    for (start, n, _, _, _) in kivi.plan_batched_write(0, 600):
+        nk = torch.from_numpy(st.k_hist[0][start:start + n].copy()).view(torch.float16).cuda()
+        nv = torch.from_numpy(st.v_hist[0][start:start + n].copy()).view(torch.float16).cuda()
+        slot = torch.zeros(n, dtype=torch.int64, device="cuda")
+        kivi.kivi_cache_write_batched_dsl(*pool, g["k_scr"][0], g["v_scr"][0], nk, nv, slot, bt,
+                                          start, n)
+    st.build_oracle()
+    torch.cuda.synchronize()
+    _compare_pool(st, g, what="batched writer")
+
+
+@pytest.mark.parametrize("name", ["tinyllama", "qwen05b", "long"])
+def test_runtime_append_multi_age_out(kivi, name):
+    """jacq_kivi_cache_append with whole histories in one launch (many
+    age-outs per sequence), page 16, HD 64/128, R 32/128 == oracle."""
+    w = wl.WORKLOADS[name].scaled(batch=3, ctx_lo=700, ctx_hi=700)
+    st = State(w, lens=[700, 700, 700])
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, st.max_pages,
+                            st.num_pages)
+    cache = kivi.PagedKiviCache(geo, st.batch)
+    nk = torch.from_numpy(np.stack(st.k_hist)).view(torch.float16).cuda()
+    nv = torch.from_numpy(np.stack(st.v_hist)).view(torch.float16).cuda()
+    bt = torch.from_numpy(st.tables).cuda()
+    cache.append(nk, nv, bt, torch.zeros(st.batch, dtype=torch.int32, device="cuda"))
+    st.build_oracle()
+    torch.cuda.synchronize()
+    g = dict(zip(("k_code", "k_scale", "k_zero", "v_code", "v_scale", "v_zero", "k_scr", "v_scr"),
+                 cache.pool()))
+    res = [700 - wl.split_old_tokens(700, w.residual)] * 3
+    _compare_pool(st, g, scratch_rows=res, what=f"append {name}")
+
+
+def test_runtime_step_writes_then_decode(kivi):
+    """Per-step writer (1 token per sequence, ragged lengths crossing age-out
+    boundaries) then decode, mistral geometry at page 16."""
+    w = wl.WORKLOADS["mistral7b"].scaled(batch=4, ctx_lo=150)
+    lens = np.array([150, 155, 159, 190])
+    st = State(w, lens=lens, extra_tokens=40)
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, st.max_pages,
+                            st.num_pages)
+    cache = kivi.PagedKiviCache(geo, st.batch)
+    bt = torch.from_numpy(st.tables).cuda()
+    hist_k = [torch.from_numpy(k).view(torch.float16).cuda() for k in st.k_hist]
+    hist_v = [torch.from_numpy(v).view(torch.float16).cuda() for v in st.v_hist]
+    for b in range(st.batch):  # per-sequence prefill through one-sequence views
+        L = int(lens[b])
+        cache.sequence_view(b).append(hist_k[b][None, :L].contiguous(),
+                                      hist_v[b][None, :L].contiguous(), bt[b:b + 1].contiguous(),
+                                      torch.zeros(1, dtype=torch.int32, device="cuda"))
+    st.build_oracle()
+    cur = lens.copy()
+    for step in range(40):
+        nk = torch.stack([hist_k[b][cur[b]] for b in range(st.batch)])[:, None].contiguous()
+        nv = torch.stack([hist_v[b][cur[b]] for b in range(st.batch)])[:, None].contiguous()
+        cache.append(nk, nv, bt, torch.from_numpy(cur.astype(np.int32)).cuda())
+        for b in range(st.batch):
+            o.cache_write(st.cache, b, st.k_hist[b][cur[b]], st.v_hist[b][cur[b]], st.tables[b],
+                          int(cur[b]) + 1)
+        cur += 1
+    torch.cuda.synchronize()
+    g = dict(zip(("k_code", "k_scale", "k_zero", "v_code", "v_scale", "v_zero", "k_scr", "v_scr"),
+                 cache.pool()))
+    res = [int(n - wl.split_old_tokens(int(n), w.residual)) for n in cur]
+    _compare_pool(st, g, scratch_rows=res, what="step writes")
+    q = torch.from_numpy(st.q).view(torch.float16).cuda()
+    out = cache.decode(q, torch.from_numpy(cur.astype(np.int32)).cuda(), bt)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), st.decode_ref(cur), "decode after step writes")
+
+
+# ---------------------------------------------------------------- decode
+
+def _decode_case(kivi, w: wl.Workload, lens, seed=0):
+    st = State(w, lens=lens, seed=seed)
+    st.build_oracle()
+    g = to_torch(st)
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, st.max_pages,
+                            st.num_pages)
+    cache = kivi.PagedKiviCache.from_tensors(geo, g)
+    q = torch.from_numpy(st.q).view(torch.float16).cuda()
+    out = cache.decode(q, torch.from_numpy(st.lens.astype(np.int32)).cuda(),
+                       torch.from_numpy(st.tables).cuda())
+    torch.cuda.synchronize()
+    return st, out.cpu().numpy()
+
+
+@pytest.mark.parametrize("name,lens", [
+    ("tinyllama", [512]),
+    ("qwen05b", [2048, 1, 33, 160, 161, 191, 192, 1000]),
+    ("mistral7b", [4096, 129, 4095]),
+    ("qwen14b", [1024, 3000, 5001]),
+    ("long", [6000, 4097]),
+])
+def test_runtime_decode_matches_twopass(kivi, name, lens):
+    w = wl.WORKLOADS[name]
+    st, out = _decode_case(kivi, w, lens)
+    assert_close(out, st.decode_ref(), f"decode {name}")
+
+
+def test_v1_jac_launch_all_boundaries(kivi):
+    """jac_launch (40/8/128, page 32) at the boundary-probe lengths."""
+    st = State(V1, lens=[4096], seed=7)
+    st.build_oracle()
+    g = to_torch(st)
+    bt = torch.from_numpy(st.tables[0]).cuda()
+    q = torch.from_numpy(st.q[0].copy()).view(torch.float16).cuda()
+    pool = [g[n] for n in ("k_code", "k_scale", "k_zero", "v_code", "v_scale", "v_zero")]
+    for L in (128, 129, 159, 160, 191, 192, 4096):
+        out = torch.empty((40, 128), dtype=torch.float32, device="cuda")
+        kivi.kivi_decode_dsl(q, bt[:max(1, (L - 128) // 32)].contiguous() if L >= 160 else bt,
+                             *pool, g["k_scr"][0], g["v_scr"][0], L, out)
+        torch.cuda.synchronize()
+        ref = o.decode_twopass(st.cache, 0, st.q[0], st.tables[0], L)
+        assert_close(out.cpu().numpy(), ref, f"jac_launch L={L}")
+
+
+def test_v1_batched_decode_equals_single(kivi):
+    """jac_launch_batched == jac_launch per query (variants.rs:1207-1215)."""
+    st = State(V1, lens=[1000], seed=8)
+    st.build_oracle()
+    g = to_torch(st)
+    bt = torch.from_numpy(st.tables[0]).cuda()
+    pool = [g[n] for n in ("k_code", "k_scale", "k_zero", "v_code", "v_scale", "v_zero")]
+    nq = 20
+    rng = np.random.default_rng(3)
+    qs = rng.standard_normal((nq, 40, 128)).astype(np.float16)
+    seq = np.arange(1000 - nq + 1, 1001).astype(np.int32)
+    qt = torch.from_numpy(qs).cuda()
+    out_b = torch.empty((nq, 40, 128), dtype=torch.float32, device="cuda")
+    kivi.kivi_decode_batched_dsl(qt, torch.from_numpy(seq).cuda(), bt, *pool, g["k_scr"][0],
+                                 g["v_scr"][0], nq, out_b)
+    for i in range(nq):
+        out = torch.empty((40, 128), dtype=torch.float32, device="cuda")
+        kivi.kivi_decode_dsl(qt[i].contiguous(), bt, *pool, g["k_scr"][0], g["v_scr"][0],
+                             int(seq[i]), out)
+        torch.cuda.synchronize()
+        assert torch.equal(out, out_b[i]), f"query {i}"
+        ref = o.decode_twopass(st.cache, 0, qs[i].view(np.uint16), st.tables[0], int(seq[i]))
+        assert_close(out.cpu().numpy(), ref, f"batched q{i}")
+
+
+def test_page16_equals_page32(kivi):
+    """Separating page from group is invisible to results: the same history
+    stored in 16-token and 32-token pages decodes identically."""
+    outs = []
+    for page in (16, 32):
+        w = wl.WORKLOADS["mistral7b"].scaled(batch=2, ctx_lo=1500, page=page)
+        st, out = _decode_case(kivi, w, [1500, 777], seed=21)
+        outs.append(out)
+    assert np.array_equal(outs[0], outs[1])
+
+
+def test_seq_len_zero_and_clamp(kivi):
+    """SEQ_LEN <= 0 gives O = 0; SEQ_LEN beyond the table's capacity is
+    clamped like the reference kernel (snapshot :74-83)."""
+    w = wl.WORKLOADS["qwen14b"].scaled(batch=2, ctx_lo=600)
+    st, _ = _decode_case(kivi, w, [600, 600])
+    g = to_torch(st)
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, st.max_pages,
+                            st.num_pages)
+    cache = kivi.PagedKiviCache.from_tensors(geo, g)
+    q = torch.from_numpy(st.q).view(torch.float16).cuda()
+    cap = geo.max_seq_len()
+    out = cache.decode(q, torch.tensor([0, cap + 1000], dtype=torch.int32, device="cuda"),
+                       torch.from_numpy(st.tables).cuda())
+    torch.cuda.synchronize()
+    o_np = out.cpu().numpy()
+    assert np.all(o_np[0] == 0)
+    ref = o.decode_twopass(st.cache, 1, st.q[1], st.tables[1], cap + 1000)
+    assert_close(o_np[1], ref, "clamped")
