@@ -1,0 +1,265 @@
+"""Benchmark of the paged int4-KIVI decode step on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload qwen14b]
+
+A step is one pass of the hot path over the batch: the cache writer appends
+one new token to every sequence (aging out 32-token groups where a sequence
+crosses the residual window), then paged decode attention runs for one query
+token per sequence.  Inputs are synthetic (seeded N(0,1) with outlier K
+channels, BASELINE workload definitions in jacq_amd/workloads.py) and resident
+in HBM before timing starts.  Each step is bracketed by HIP events on the
+stream the kernels run on; a 512 MiB buffer is written before every step so
+the 256 MiB MALL and the L2 start cold.
+
+Prints ONE JSON line.  `value` is the effective KV bandwidth of the decode
+(algorithmic bytes / decode time, GB/s); `ms_per_step` is the decode time per
+step.  The CPU baseline runs the oracle (oracle/, a C restatement of the
+reference path) over the same state on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="qwen14b")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-flush", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the decode path shards by sequence or kv head with no exchange; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from jacq_amd import kivi, layout, workloads as wl
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    w = wl.WORKLOADS[args.workload]
+    rng = np.random.default_rng(w.seed)
+    lens0 = wl.context_lens(w, rng)            # lengths when timing starts (after prefill)
+    total_steps = args.warmup + args.steps
+    tables_np, num_pages, max_pages = wl.block_tables(w, lens0 + total_steps + 1, rng)
+    outl = wl.outlier_channels(w, rng)
+    B = w.batch
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, w.group, w.residual, max_pages, num_pages)
+    cache = kivi.PagedKiviCache(geo, B, dev)
+    bt = torch.from_numpy(tables_np).to(dev)
+    gen = torch.Generator(device=dev).manual_seed(1000 + w.seed)
+
+    # ---- build the cache state on the GPU with the writer ----
+    t0 = time.time()
+    prefill = w.prefill_chunk
+    for b in range(B):
+        L = int(lens0[b]) - prefill
+        k, v = wl.kv_tokens_torch(w, gen, L, outl, dev)
+        cache.sequence_view(b).append(k[None].contiguous(), v[None].contiguous(),
+                                      bt[b:b + 1].contiguous(),
+                                      torch.zeros(1, dtype=torch.int32, device=dev))
+        del k, v
+    torch.cuda.synchronize()
+    prefill_info = None
+    if prefill:
+        # one launch: every sequence appends a `prefill`-token chunk (many age-outs each)
+        k, v = wl.kv_tokens_torch(w, gen, B * prefill, outl, dev)
+        k = k.view(B, prefill, w.nkv, w.hd).contiguous()
+        v = v.view(B, prefill, w.nkv, w.hd).contiguous()
+        start = torch.from_numpy((lens0 - prefill).astype(np.int32)).to(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        cache.append(k, v, bt, start)
+        e1.record()
+        torch.cuda.synchronize()
+        prefill_info = {"tokens_per_seq": prefill, "us": round(e0.elapsed_time(e1) * 1e3, 1)}
+        del k, v
+    log(f"[bench] state built in {time.time() - t0:.1f}s: B={B} ctx {lens0.min()}..{lens0.max()} "
+        f"pages={num_pages}")
+
+    # ---- per-step inputs ----
+    qs = torch.randn((total_steps, B, w.nh, w.hd), generator=gen, device=dev).half()
+    nk = torch.randn((total_steps, B, 1, w.nkv, w.hd), generator=gen, device=dev).half()
+    nv = torch.randn((total_steps, B, 1, w.nkv, w.hd), generator=gen, device=dev).half()
+    out = torch.empty((B, w.nh, w.hd), dtype=torch.float32, device=dev)
+    lens_before = torch.from_numpy(lens0.astype(np.int32)).to(dev)
+    lens_after = lens_before + 1
+    flush = None if args.no_flush else torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    ws_bytes = kivi.lib().jacq_kivi_decode_workspace_size(ctypes_geo(kivi, geo), B)
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(total_steps)]
+    stream = torch.cuda.current_stream(dev)
+    torch.cuda.synchronize()
+    wall0 = None
+    for i in range(total_steps):
+        if i == args.warmup:
+            torch.cuda.synchronize()
+            wall0 = time.perf_counter()
+        if flush is not None:
+            flush.fill_(i & 0xff)
+        e = evs[i]
+        e[0].record(stream)
+        cache.append(nk[i], nv[i], bt, lens_before)
+        e[1].record(stream)
+        cache.decode(qs[i], lens_after, bt, out=out, workspace=workspace)
+        e[2].record(stream)
+        lens_before.add_(1)
+        lens_after.add_(1)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+
+    dec_ms, wr_ms, step_bytes = [], [], []
+    for i in range(args.warmup, total_steps):
+        e = evs[i]
+        wr_ms.append(e[0].elapsed_time(e[1]))
+        dec_ms.append(e[1].elapsed_time(e[2]))
+        step_bytes.append(layout.decode_step_bytes(lens0 + i + 1, w.nh, w.nkv, w.hd, w.page,
+                                                   w.residual, w.group))
+    dec = np.array(dec_ms)
+    wr = np.array(wr_ms)
+    gbs = float(np.sum(step_bytes) / (dec.sum() * 1e-3) / 1e9)
+    bytes_per_step = float(np.mean(step_bytes))
+
+    # ---- CPU baseline: the oracle over the same final state on this host ----
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(args, w, cache, qs[total_steps - 1], lens0 + total_steps, tables_np,
+                           out, max_pages, bytes_per_step_last=step_bytes[-1])
+
+    traffic = load_traffic(args.workload)
+    line = {
+        "metric": "paged int4-KIVI decode attn us/step + effective KV GB/s (% HBM peak), 14B shape",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(float(dec.mean()), 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{w.name}: {w.nh}q/{w.nkv}kv heads, head_dim {w.hd}, batch {B}, "
+                        f"context U[{w.ctx_lo},{w.ctx_hi}], page {w.page}, group {w.group}, "
+                        f"residual {w.residual}, int4 KIVI K/V, fused cache write + decode",
+            "batch": B,
+            "mean_context": float(np.mean(lens0)),
+            "pages": num_pages,
+            "cold_cache": flush is not None,
+        },
+        "decode_us": {"mean": round(float(dec.mean()) * 1e3, 2),
+                      "min": round(float(dec.min()) * 1e3, 2),
+                      "median": round(float(np.median(dec)) * 1e3, 2),
+                      "p90": round(float(np.percentile(dec, 90)) * 1e3, 2)},
+        "write_us": {"mean": round(float(wr.mean()) * 1e3, 2),
+                     "median": round(float(np.median(wr)) * 1e3, 2)},
+        "step_us_write_plus_decode": round(float((dec + wr).mean()) * 1e3, 2),
+        "decode_bytes_per_step": int(bytes_per_step),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "wall_s_timed_region": round(wall, 4),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+    }
+    if prefill_info:
+        line["prefill_write"] = prefill_info
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def ctypes_geo(kivi, geo):
+    import ctypes
+    return ctypes.byref(geo.c())
+
+
+def load_traffic(workload: str):
+    """HBM bytes per decode launch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), if one exists."""
+    p = os.path.join(ROOT, "profiles", f"decode_{workload}_traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get("traffic_bytes_per_launch")
+
+
+def cpu_baseline(args, w, cache, q_last, lens_last, tables_np, gpu_out, max_pages,
+                 bytes_per_step_last):
+    """Time the oracle's batched decode on the host over the final GPU state."""
+    import torch
+
+    from oracle import oracle as o
+    from tests.kivi_testlib import ATOL, RTOL
+
+    o.lib()
+
+    def host(t):
+        x = t.detach().cpu()
+        if x.dtype == torch.float16:
+            return x.view(torch.int16).numpy().view(np.uint16)
+        return x.numpy()
+
+    g = o.Geometry(w.nh, w.nkv, w.hd, w.page, w.group, w.residual, max_pages)
+    c = o.Cache(g, host(cache.k_code), host(cache.k_scale), host(cache.k_zero),
+                host(cache.v_code), host(cache.v_scale), host(cache.v_zero),
+                host(cache.k_scr), host(cache.v_scr))
+    q = host(q_last)
+    lens = lens_last.astype(np.int32)
+    threads = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
+    t0 = time.perf_counter()
+    ref = o.decode_batch(c, q, lens, tables_np, nthreads=threads)
+    dt = time.perf_counter() - t0
+    # sanity: the GPU's last step saw the same state and query
+    gpu = gpu_out.cpu().numpy()
+    err = np.abs(gpu - ref)
+    ok = bool(np.all(err <= ATOL + RTOL * np.abs(ref)))
+    return {
+        "value": round(bytes_per_step_last / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"full last step: {w.batch} sequences, one decode query each, "
+                  f"{int(lens.sum())} tokens; {dt * 1e3:.1f} ms on {threads} threads "
+                  f"(OpenMP over sequence x kv head)",
+        "us_per_step": round(dt * 1e6, 1),
+        "matches_gpu_within_tolerance": ok,
+        "max_abs_diff_vs_gpu": float(err.max()),
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libjacq_kivi.so")
-SOURCES = ["kivi_api.hip", "kivi_writer.hip", "kivi_decode.hip"]
+SOURCES = ["kivi_api.hip", "kivi_writer.hip", "kivi_decode.hip", "kivi_decode_mfma.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

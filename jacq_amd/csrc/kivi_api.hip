@@ -33,6 +33,10 @@ int fail(int code, const std::string& msg) {
 constexpr jacq_kivi_geometry kGlobal = {40, 8, 128, 32, 32, 128, 124, INT32_MAX};
 constexpr jacq_kivi_geometry kTp2Local = {20, 4, 128, 32, 32, 128, 124, INT32_MAX};
 
+int64_t max_seq_len(const jacq_kivi_geometry& x) {
+  return ((int64_t)x.max_pages_per_seq * x.page_size / jacq::kGroup) * jacq::kGroup + x.residual;
+}
+
 int check_geometry(const jacq_kivi_geometry* x) {
   if (!x) return fail(JACQ_KIVI_EINVAL, "geometry pointer is null");
   if (x->num_heads < 1 || x->num_kv_heads < 1 || x->num_heads % x->num_kv_heads != 0)
@@ -55,6 +59,8 @@ int check_geometry(const jacq_kivi_geometry* x) {
   if (x->max_pages_per_seq < 0) return fail(JACQ_KIVI_EINVAL, "max_pages_per_seq must be >= 0");
   if (x->num_pages < 1)
     return fail(JACQ_KIVI_EINVAL, "num_pages (page storage capacity) must be positive");
+  if (jacq::split_count(max_seq_len(*x)) > 64)
+    return fail(JACQ_KIVI_EINVAL, "block table addresses more than 64 x 4096 tokens per sequence");
   return JACQ_KIVI_OK;
 }
 
@@ -71,10 +77,6 @@ KiviGeo make_geo(const jacq_kivi_geometry& x) {
   g.rs = x.residual + jacq::kGroup;
   g.lq = (int)(((int64_t)x.max_pages_per_seq * x.page_size / jacq::kGroup) * jacq::kGroup);
   return g;
-}
-
-int64_t max_seq_len(const jacq_kivi_geometry& x) {
-  return ((int64_t)x.max_pages_per_seq * x.page_size / jacq::kGroup) * jacq::kGroup + x.residual;
 }
 
 // ---- device properties and the library-owned split-K workspace ----
@@ -124,30 +126,36 @@ int library_workspace(int dev, size_t bytes, void** out) {
 }
 
 // Split slots per (sequence, kv head): split_plan never makes more than
-// min(kMaxSplits, ceil(n / kSplitTarget)) splits, which grows with n, so the
-// longest sequence the call can see bounds every sequence's count.
+// split_count(n) splits, which grows with n, so the longest sequence the call
+// can see bounds every sequence's count.
 struct SplitPlan {
   int max_splits;
 };
 
-SplitPlan plan_splits(int64_t max_tokens) {
-  int64_t s = (max_tokens + jacq::kSplitTarget - 1) / jacq::kSplitTarget;
-  if (s < 1) s = 1;
-  if (s > jacq::kMaxSplits) s = jacq::kMaxSplits;
-  return {(int)s};
-}
+SplitPlan plan_splits(int64_t max_tokens) { return {jacq::split_count(max_tokens)}; }
 
+// Workspace: [m,l fp32][acc fp32] per (sequence, kv head, split, head).
 size_t workspace_bytes(const KiviGeo& g, int batch, const SplitPlan& sp) {
   if (sp.max_splits <= 1) return 0;
   const size_t slots = (size_t)batch * g.nkv * sp.max_splits * g.gqa;
-  return slots * (size_t)(g.hd + 2) * sizeof(float) + 256;
+  return slots * (size_t)(g.hd + 2) * sizeof(float);
 }
 
 void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& sp, void* ws) {
   a.max_splits = sp.max_splits;
   const size_t slots = (size_t)batch * g.nkv * sp.max_splits * g.gqa;
-  a.ws_acc = (float*)ws;
-  a.ws_ml = ws ? (float*)ws + slots * g.hd : nullptr;
+  a.ws_ml = (float*)ws;
+  a.ws_acc = ws ? a.ws_ml + slots * 2 : nullptr;
+}
+
+// JACQ_KIVI_DECODE=simple selects the VALU decode kernel (a cross-check of
+// the matrix-core kernel); the default is the matrix-core kernel.
+bool use_simple_decode() {
+  static const bool simple = [] {
+    const char* e = std::getenv("JACQ_KIVI_DECODE");
+    return e && std::string(e) == "simple";
+  }();
+  return simple;
 }
 
 // Decode with a runtime geometry; seq_len_host >= 0 when the (single) length
@@ -197,8 +205,9 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
   a.out = O;
   a.out_stride = (int64_t)g.nh * g.hd;
   fill_ws(a, g, batch, sp, need > 0 ? ws : nullptr);
-  if (jacq::launch_decode(g, a, batch, stream) != hipSuccess)
-    return fail(JACQ_KIVI_EHIP, "decode launch failed");
+  const hipError_t e = use_simple_decode() ? jacq::launch_decode(g, a, batch, stream)
+                                            : jacq::launch_decode_mfma(g, a, batch, stream);
+  if (e != hipSuccess) return fail(JACQ_KIVI_EHIP, "decode launch failed");
   return JACQ_KIVI_OK;
 }
 

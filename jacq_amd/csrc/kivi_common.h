@@ -51,16 +51,25 @@ __host__ __device__ inline void decode_window(const KiviGeo& g, int seq_len, int
 }
 
 // Split-K plan of one sequence of n tokens: about kSplitTarget tokens per
-// split, at most kMaxSplits splits, chunks of whole 32-token groups.  It
-// depends on n alone, so a sequence decodes to the same bits whatever else
-// is in the batch (single and batched calls agree exactly).
+// split, at most kMaxSplits splits unless that would make a split longer
+// than kMaxSplitTokens, chunks of whole 32-token groups.  It depends on n
+// alone, so a sequence decodes to the same bits whatever else is in the batch
+// (single and batched calls agree exactly).
 constexpr int kSplitTarget = 512;
 constexpr int kMaxSplits = 16;
+constexpr int kMaxSplitTokens = 4096;
+
+__host__ __device__ inline int split_count(long long n) {
+  long long s = (n + kSplitTarget - 1) / kSplitTarget;
+  if (s > kMaxSplits) s = kMaxSplits;
+  const long long s_min = (n + kMaxSplitTokens - 1) / kMaxSplitTokens;
+  if (s < s_min) s = s_min;
+  if (s < 1) s = 1;
+  return (int)s;
+}
 
 __host__ __device__ inline void split_plan(int n, int* nsplit, int* chunk) {
-  int s = (n + kSplitTarget - 1) / kSplitTarget;
-  if (s < 1) s = 1;
-  if (s > kMaxSplits) s = kMaxSplits;
+  const int s = split_count(n);
   int c = (n + s - 1) / s;
   c = ((c + kGroup - 1) / kGroup) * kGroup;
   if (c < kGroup) c = kGroup;

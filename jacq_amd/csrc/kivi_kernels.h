@@ -50,5 +50,7 @@ struct DecodeArgs {
 
 hipError_t launch_append(const KiviGeo& g, const AppendArgs& a, int batch, hipStream_t stream);
 hipError_t launch_decode(const KiviGeo& g, const DecodeArgs& a, int batch, hipStream_t stream);
+hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
+                              hipStream_t stream);
 
 }  // namespace jacq
