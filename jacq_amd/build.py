@@ -27,6 +27,8 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # IEEE fp32 division for the writer's scale / code arithmetic.
     "-fhip-fp32-correctly-rounded-divide-sqrt",
+    # keep MFMA accumulators in VGPRs (no per-iteration AGPR <-> VGPR copies)
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-I", os.path.join(ROOT, "include"),
     "-I", CSRC,
 ]

@@ -134,20 +134,6 @@ struct SplitPlan {
 
 SplitPlan plan_splits(int64_t max_tokens) { return {jacq::split_count(max_tokens)}; }
 
-// Workspace: [m,l fp32][acc fp32] per (sequence, kv head, split, head).
-size_t workspace_bytes(const KiviGeo& g, int batch, const SplitPlan& sp) {
-  if (sp.max_splits <= 1) return 0;
-  const size_t slots = (size_t)batch * g.nkv * sp.max_splits * g.gqa;
-  return slots * (size_t)(g.hd + 2) * sizeof(float);
-}
-
-void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& sp, void* ws) {
-  a.max_splits = sp.max_splits;
-  const size_t slots = (size_t)batch * g.nkv * sp.max_splits * g.gqa;
-  a.ws_ml = (float*)ws;
-  a.ws_acc = ws ? a.ws_ml + slots * 2 : nullptr;
-}
-
 // JACQ_KIVI_DECODE=simple selects the VALU decode kernel (a cross-check of
 // the matrix-core kernel); the default is the matrix-core kernel.
 bool use_simple_decode() {
@@ -156,6 +142,30 @@ bool use_simple_decode() {
     return e && std::string(e) == "simple";
   }();
   return simple;
+}
+
+// Partial-result slots: VALU kernel -- one per (sequence, kv head, split);
+// matrix-core kernel -- one per (sequence, kv head) plus one per wavefront
+// (a wavefront's run cuts at most one extra piece off the stream).
+size_t partial_slots(const KiviGeo& g, int batch, const SplitPlan& sp, int waves) {
+  if (use_simple_decode())
+    return sp.max_splits <= 1 ? 0 : (size_t)batch * g.nkv * sp.max_splits;
+  return (size_t)batch * g.nkv + (size_t)waves;
+}
+
+// Workspace: [m,l fp32 per slot and head][acc fp32 per slot, head, channel].
+size_t workspace_bytes(const KiviGeo& g, int batch, const SplitPlan& sp, int waves) {
+  return partial_slots(g, batch, sp, waves) * g.gqa * (size_t)(g.hd + 2) * sizeof(float);
+}
+
+void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& sp, int waves,
+             void* ws) {
+  a.max_splits = sp.max_splits;
+  a.batch = batch;
+  a.waves = waves;
+  const size_t slots = partial_slots(g, batch, sp, waves) * g.gqa;
+  a.ws_ml = (float*)ws;
+  a.ws_acc = ws ? a.ws_ml + slots * 2 : nullptr;
 }
 
 // Decode with a runtime geometry; seq_len_host >= 0 when the (single) length
@@ -176,7 +186,8 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
     max_tokens = ov + rv;
   }
   const SplitPlan sp = plan_splits(max_tokens);
-  const size_t need = workspace_bytes(g, batch, sp);
+  const int waves = jacq::decode_stream_waves(g_dev[dev].cus);
+  const size_t need = workspace_bytes(g, batch, sp, waves);
   if (need > 0) {
     if (ws == nullptr) {
       if (int e = library_workspace(dev, need, &ws)) return e;
@@ -204,7 +215,7 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
   a.scr_stride = scr_stride;
   a.out = O;
   a.out_stride = (int64_t)g.nh * g.hd;
-  fill_ws(a, g, batch, sp, need > 0 ? ws : nullptr);
+  fill_ws(a, g, batch, sp, waves, need > 0 ? ws : nullptr);
   const hipError_t e = use_simple_decode() ? jacq::launch_decode(g, a, batch, stream)
                                             : jacq::launch_decode_mfma(g, a, batch, stream);
   if (e != hipSuccess) return fail(JACQ_KIVI_EHIP, "decode launch failed");
@@ -287,7 +298,8 @@ size_t jacq_kivi_decode_workspace_size(const jacq_kivi_geometry* geo, int32_t ba
   int dev = 0;
   if (current_device(&dev) != JACQ_KIVI_OK) return 0;
   const KiviGeo g = make_geo(*geo);
-  return workspace_bytes(g, batch, plan_splits(max_seq_len(*geo)));
+  return workspace_bytes(g, batch, plan_splits(max_seq_len(*geo)),
+                         jacq::decode_stream_waves(g_dev[dev].cus));
 }
 
 int jacq_kivi_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q, const int32_t* SEQ_LENS,

@@ -45,12 +45,16 @@ struct DecodeArgs {
   int64_t out_stride;
   float* ws_ml;   // [batch, NKV, max_splits, G, 2]  (m, l)
   float* ws_acc;  // [batch, NKV, max_splits, G, HD]
-  int max_splits;  // split slots per (sequence, kv head): grid.x and workspace stride
+  int max_splits;  // VALU kernel: split slots per (sequence, kv head)
+  int batch;       // sequences (queries) in the call
+  int waves;       // matrix-core kernel: wavefronts sharing the tile stream
 };
 
 hipError_t launch_append(const KiviGeo& g, const AppendArgs& a, int batch, hipStream_t stream);
 hipError_t launch_decode(const KiviGeo& g, const DecodeArgs& a, int batch, hipStream_t stream);
 hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
                               hipStream_t stream);
+// wavefronts the matrix-core decode launches on a device with `cus` CUs
+int decode_stream_waves(int cus);
 
 }  // namespace jacq
