@@ -34,6 +34,7 @@
 //          V = code * s_t + z_t is dequantised with one packed-fp16 FMA per
 //          two values, and sum_t P z_t accumulates in one extra MFMA per group.
 #include <type_traits>
+#include <utility>
 
 #include "kivi_kernels.h"
 
@@ -96,11 +97,6 @@ __device__ inline u32x4 perm_pairs(u32x4 d) {
   return r;
 }
 
-// True when both fp16 values of a pair have magnitude below 64.
-__device__ inline bool small_pair(uint32_t v) {
-  return (v & 0x7FFFu) < 0x5400u && ((v >> 16) & 0x7FFFu) < 0x5400u;
-}
-
 template <int HD, int P>
 struct Cfg {
   static constexpr int KS = HD / 32;       // k-steps of the QK^T product
@@ -113,91 +109,225 @@ struct Cfg {
   typedef typename std::conditional<HD == 128, u32x2, uint32_t>::type pvec;
 };
 
-// Per-lane offsets inside a 32-token group, fixed for the whole kernel.
+// Token <-> MFMA position maps of a quantised group.  The QK^T A operand
+// row c of tile tt holds token tok_k(tt, c); the PV K index 8j + e (lane
+// quarter j, element e) is token tok_v(j, e).  They agree -- S^T row 4j + i of
+// tile tt lands in lane quarter j, element 4tt + i -- so P leaves the softmax
+// already in PV A-operand order.  Within a 32-lane half the 16 rows a V read
+// touches alternate in parity, which keeps ds_read_b32 free of bank conflicts
+// on the row-major LDS image of the codes.
+__device__ constexpr int tok_k(int tt, int c) {
+  return 8 * tt + 2 * (c & 3) + ((c >> 2) & 1) + 16 * (c >> 3);
+}
+__device__ constexpr int tok_v(int j, int e) { return 2 * e + (j & 1) + 16 * (j >> 1); }
+
+// Per-lane LDS read offsets inside a stage, fixed for the whole kernel.
 struct LaneMap {
-  int kpg[2], koff[2];  // K tile tt: page within the group, byte offset in the page
-  int vpg, voff;        // V rows 8j..8j+7: page within the group, byte offset
-  int spg, soff;        // V scale/zero of token lane%32: page within the group, element offset
-  int ksoff;            // K scale/zero: element offset in the page's row
+  int kread[2];  // K codes of tile tt: row tok_k(tt, c), channel block j
+  int vread;     // V codes: row tok_v(j, 0), channels CPL*c..; element e adds 2e rows
+  int vsread;    // V scale of (token tok_v(j, 0), group of channel CPL*c)
 };
 
 template <int HD, int P>
 __device__ inline LaneMap lane_map(int lane) {
   using C = Cfg<HD, P>;
-  const int c = lane & 15, j = lane >> 4, t = lane & 31;
+  const int c = lane & 15, j = lane >> 4;
   LaneMap m;
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const int tau = 8 * (c >> 2) + 4 * tt + (c & 3);  // token of MFMA row c in tile tt
-    m.kpg[tt] = tau / P;
-    m.koff[tt] = (tau % P) * C::HDP + j * C::KCB;
-  }
-  m.vpg = (8 * j) / P;
-  m.voff = ((8 * j) % P) * C::HDP + c * (C::CPL / 2);
-  m.spg = t / P;
-  m.soff = (t % P) * C::HDG;
-  m.ksoff = (HD / 32) * t;
+  for (int tt = 0; tt < 2; ++tt) m.kread[tt] = tok_k(tt, c) * C::HDP + j * C::KCB;
+  m.vread = tok_v(j, 0) * C::HDP + c * (C::CPL / 2);
+  m.vsread = 2 * (tok_v(j, 0) * C::HDG + (C::CPL * c) / kGroup);
   return m;
 }
 
-// One quantised 32-token group in flight.  The K and V codes go straight
-// from global memory to this wave's LDS buffer (global_load_lds), each lane
-// loading exactly the bytes it later feeds to the MFMAs, so the reads back
-// are contiguous per lane; the scale / zero words travel in registers.
-template <int HD, int P>
-struct Stage {
-  typename Cfg<HD, P>::pvec ksz;  // K scale (lanes < 32) / zero (lanes >= 32)
-  typename Cfg<HD, P>::pvec vsz;  // V scale / zero of token lane%32, every channel group
-};
-
-// LDS image of one group's codes: [tile][lane] K bytes, [row][lane] V bytes.
-// global_load_lds places lane i's data at byte 16*i for 16-byte loads and at
-// byte 4*i for loads of 4 bytes or fewer.
+// One quantised 32-token group of one kv head in LDS.  Codes keep the cache's
+// row-major order (token rows of HD/2 bytes); scales and zeros arrive as
+//   s[0, 2HD)        K scale of channel d at 2d
+//   s[2HD, 4HD)      K zero
+//   s[4HD, ..)       V scale of (token t, group g) at 2(t*HDG + g), then V zero.
+// Everything comes by LDS DMA with 16 bytes per lane (global_load_lds_dwordx4
+// puts lane i's bytes at 16i): an LDS DMA costs about the same issue time
+// whatever its width, so a group is 2 * 32*HD/2 / 1024 + 1 of them.  The DMAs
+// are issued from inline asm and waited for with explicit vmcnt counts: a
+// ring of stages keeps S - 1 groups in flight while one is computed.
 template <int HD>
-struct CodeBuf {
-  uint8_t k[2][64 * (HD / 8)];
-  uint8_t v[8][64 * 4];
+struct StageBuf {
+  uint8_t k[32 * HD / 2];
+  uint8_t v[32 * HD / 2];
+  uint8_t s[4 * HD + 128 * (HD / kGroup)];
 };
 
-struct StageBases {  // per-lane pointers with the kv head folded in
-  const uint8_t* kcode;
-  const uint8_t* vcode;
-  const uint16_t* ksz;  // k_scale or k_zero by lane half
-  const uint16_t* vsz;  // v_scale or v_zero by lane half
-  uint32_t code_page;   // bytes per physical page of K or V codes (all kv heads)
-  uint32_t vsz_page;    // elements per physical page of V scales
-  uint32_t ksz_page;    // elements per physical page of K scales
-};
+template <int HD>
+constexpr int code_dmas() {  // 1 KiB DMAs per K or V code block
+  return 32 * HD / 2 / 1024;
+}
 
-typedef const __attribute__((address_space(1))) void* gptr_t;
-typedef __attribute__((address_space(3))) void* lptr_t;
+// vector memory instructions one stage issues (vmcnt units)
+template <int HD>
+constexpr int stage_loads() {
+  return 2 * code_dmas<HD>() + 1;
+}
+
+// Per-segment DMA sources.  Codes: wave-uniform bases (kv head folded in);
+// scales: the lane's own 16-byte word of page 0 and the page stride of its
+// array (K scales live once per group, in its first page).
+struct StageBases {
+  uint64_t kc, vc;     // k_code / v_code + head offset (uniform)
+  uint32_t code_page;  // bytes per physical page of K or V codes (all kv heads)
+  uint64_t sc;         // lane's scale / zero source in page 0
+  uint32_t sc_page;    // lane's page stride in bytes
+  bool sc_p1;          // lane's word lies in the group's second page
+  bool sc_on;          // lane takes part in the scale DMA
+};
 
 template <int HD, int P>
-__device__ inline void load_stage(Stage<HD, P>& st, CodeBuf<HD>* buf, const StageBases& sb,
-                                  const LaneMap& lm, uint32_t p0, uint32_t p1) {
+__device__ inline StageBases stage_bases(const DecodeArgs& a, int nkv, int h, int lane) {
   using C = Cfg<HD, P>;
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const uint32_t phys = lm.kpg[tt] ? p1 : p0;
-    const uint8_t* src = sb.kcode + (uint64_t)phys * sb.code_page + lm.koff[tt];
-    if constexpr (HD == 128) {
-      __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)buf->k[tt], 16, 0, 0);
-    } else {
-      __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)buf->k[tt], 4, 0, 0);
-      __builtin_amdgcn_global_load_lds((gptr_t)(src + 4), (lptr_t)(buf->k[tt] + 256), 4, 0, 0);
+  constexpr int KL = HD / 8;          // lanes per K scale (or zero) row
+  constexpr int VL = 4 * C::HDG;      // lanes per V scale (or zero) block of 32 tokens
+  StageBases sb;
+  sb.code_page = (uint32_t)(nkv * P * C::HDP);
+  sb.kc = (uint64_t)(a.k_code + (int64_t)h * P * C::HDP);
+  sb.vc = (uint64_t)(a.v_code + (int64_t)h * P * C::HDP);
+  sb.sc_on = lane < 2 * KL + 2 * VL;
+  sb.sc_p1 = false;
+  if (lane < 2 * KL) {
+    const uint16_t* arr = lane < KL ? a.k_scale : a.k_zero;
+    sb.sc = (uint64_t)(arr + (int64_t)h * HD + 8 * (lane % KL));
+    sb.sc_page = (uint32_t)(nkv * HD * 2);
+  } else {
+    const int l = (lane - 2 * KL) % VL;
+    const uint16_t* arr = lane < 2 * KL + VL ? a.v_scale : a.v_zero;
+    const int t = 8 * l / C::HDG;  // first token of the lane's word
+    sb.sc_p1 = t >= P;
+    sb.sc = (uint64_t)(arr + ((int64_t)h * P + t % P) * C::HDG);
+    sb.sc_page = (uint32_t)(nkv * P * C::HDG * 2);
+  }
+  return sb;
+}
+
+__device__ inline uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// LDS DMA of SZ bytes per lane from addr + OFF to LDS byte dst + lane * max(SZ, 4),
+// non-temporal: every cache byte is read once per decode step, and streaming
+// it past the caches sustains a markedly higher HBM read rate.
+// The instruction's immediate offset moves the LDS address as well as the
+// global one, so M0 gets dst - OFF.  M0 is set inside the same asm statement,
+// so nothing the compiler keeps in M0 is live across it.
+template <int SZ, int OFF>
+__device__ inline void dma(uint64_t addr, uint32_t dst) {
+  static_assert(OFF >= 0 && OFF < 4096, "global immediate offset range");
+  const uint32_t m0 = dst - OFF;
+  if constexpr (SZ == 16)
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off offset:%2 nt"
+                 :: "s"(m0), "v"(addr), "n"(OFF) : "memory", "m0");
+  else if constexpr (SZ == 4)
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off offset:%2 nt"
+                 :: "s"(m0), "v"(addr), "n"(OFF) : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_ushort %1, off offset:%2 nt"
+                 :: "s"(m0), "v"(addr), "n"(OFF) : "memory", "m0");
+}
+
+// The same with a wave-uniform 64-bit base in SGPRs and a 32-bit lane offset.
+template <int OFF>
+__device__ inline void dma16s(uint64_t sbase, uint32_t voff, uint32_t dst) {
+  static_assert(OFF >= 0 && OFF < 4096, "global immediate offset range");
+  const uint32_t m0 = dst - OFF;
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2 offset:%3 nt"
+               :: "s"(m0), "v"(voff), "s"(sbase), "n"(OFF) : "memory", "m0");
+}
+
+template <int N>
+__device__ inline void wait_vm() {  // at most N vector memory ops outstanding
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+template <class F, int... I>
+__device__ inline void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ inline void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Wait until `later` stages (issued after the one about to be read) remain.
+template <int L, int S>
+__device__ inline void wait_stages(int later) {
+  if constexpr (S >= 4) {
+    if (later >= 2) {
+      wait_vm<2 * L>();
+      return;
     }
   }
-  {
-    const uint32_t phys = lm.vpg ? p1 : p0;
-    const uint8_t* base = sb.vcode + (uint64_t)phys * sb.code_page + lm.voff;
-#pragma unroll
-    for (int r = 0; r < 8; ++r)
-      __builtin_amdgcn_global_load_lds((gptr_t)(base + r * C::HDP), (lptr_t)buf->v[r],
-                                       C::CPL / 2, 0, 0);
+  if (later >= 1)
+    wait_vm<L>();
+  else
+    wait_vm<0>();
+}
+
+// LDS stages per wave: S - 1 groups in flight while one is computed.
+constexpr int kStages = 3;
+static_assert(kStages >= 2 && kStages <= 4, "wait_stages covers up to 3 stages in flight");
+
+// Issue the DMAs of one group whose tokens 0..P-1 sit in page p0 and the
+// rest (page size 16) in p1.
+template <int HD, int P>
+__device__ inline void load_stage(StageBuf<HD>* buf, const StageBases& sb, uint32_t p0,
+                                  uint32_t p1, int lane) {
+  using C = Cfg<HD, P>;
+  const uint32_t base = lds_addr(buf);
+  const uint32_t kd = base + (uint32_t)offsetof(StageBuf<HD>, k);
+  const uint32_t vd = base + (uint32_t)offsetof(StageBuf<HD>, v);
+  const uint32_t lo = 16u * (uint32_t)lane;
+  if constexpr (HD == 128) {
+    // 1 KiB = 16 token rows per DMA: rows 0-15 and 16-31
+    const uint64_t o0 = (uint64_t)p0 * sb.code_page;
+    const uint64_t o1 = P == 16 ? (uint64_t)p1 * sb.code_page : o0 + 1024;
+    dma16s<0>(sb.kc + o0, lo, kd);
+    dma16s<0>(sb.kc + o1, lo, kd + 1024);
+    dma16s<0>(sb.vc + o0, lo, vd);
+    dma16s<0>(sb.vc + o1, lo, vd + 1024);
+  } else if constexpr (P == 32) {
+    const uint64_t o0 = (uint64_t)p0 * sb.code_page;
+    dma16s<0>(sb.kc + o0, lo, kd);
+    dma16s<0>(sb.vc + o0, lo, vd);
+  } else {
+    // one DMA spans both pages: lanes 0-31 rows 0-15 of p0, lanes 32-63 of p1
+    const uint64_t o = (uint64_t)(lane < 32 ? p0 : p1) * sb.code_page + (lo & 511u);
+    dma<16, 0>(sb.kc + o, kd);
+    dma<16, 0>(sb.vc + o, vd);
   }
-  st.ksz = *(const typename C::pvec*)(sb.ksz + (uint64_t)p0 * sb.ksz_page + lm.ksoff);
-  const uint32_t sphys = lm.spg ? p1 : p0;
-  st.vsz = *(const typename C::pvec*)(sb.vsz + (uint64_t)sphys * sb.vsz_page + lm.soff);
+  const uint32_t sd = base + (uint32_t)offsetof(StageBuf<HD>, s);
+  const uint64_t sa = sb.sc + (uint64_t)(sb.sc_p1 ? p1 : p0) * sb.sc_page;
+  if (sb.sc_on) dma<16, 0>(sa, sd);
+}
+
+// IEEE maximum (llvm.maximum): lowers to v_maximum3_f32 without the
+// canonicalising moves that fmaxf needs in IEEE mode.
+__device__ inline float max3f(float a, float b, float c) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+__device__ inline float max2f(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+// max with lane l ^ 16 / l ^ 32 by v_permlane16_swap / v_permlane32_swap
+// (all VALU, no LDS round trip).  Both operands start as x; after the swap one
+// holds this lane's row value and the other the partner row's.  Written as
+// asm with both operands read-write: the compiler's lowering of the builtin
+// reads the first result register for both results.  The s_nop gives the
+// VALU write of x the wait states the swap needs.
+__device__ inline float max_xor16(float x) {
+  float a = x, b = x;
+  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return max2f(a, b);
+}
+__device__ inline float max_xor32(float x) {
+  float a = x, b = x;
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return max2f(a, b);
 }
 
 template <int HD>
@@ -229,11 +359,12 @@ __device__ inline void rescale(WaveState<HD>& st, float corr, int j) {
 template <int HD>
 __device__ inline half8_t softmax_tile(WaveState<HD>& st, floatx4 s0, floatx4 s1, float kscale,
                                        float kbias, int j) {
-  const float raw = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
-                          fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+  // max over the lane's 8 scores, then over the 4 lanes of head c (lanes
+  // c, c+16, c+32, c+48) with the row-swap permutes (no LDS round trip)
+  const float raw = max3f(max3f(s0[0], s0[1], s0[2]), max3f(s0[3], s1[0], s1[1]), max2f(s1[2], s1[3]));
   float mx = __builtin_fmaf(raw, kscale, kbias);
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  mx = max_xor16(mx);
+  mx = max_xor32(mx);
   if (__builtin_amdgcn_ballot_w64(mx > st.m + kRescaleThreshold)) {
     const float m_new = fmaxf(st.m, mx);
     const float corr = __builtin_amdgcn_exp2f(st.m - m_new);
@@ -259,43 +390,48 @@ __device__ inline half8_t softmax_tile(WaveState<HD>& st, floatx4 s0, floatx4 s1
 }
 
 // Dequantise the lane's V channels CPL*c + 2k (low nibbles) and + 2k + 1
-// (high nibbles) for its 8 tokens and accumulate PV.  kBig: some |scale| >= 64,
-// where -1024 * scale overflows fp16; then the offset is removed with an
-// exact subtraction first.
-template <int HD, bool kBig>
+// (high nibbles) for its 8 tokens and accumulate PV.  x = 1024 + code (exact
+// fp16) gives code * s = fma(x, s, -1024 s) in one rounding.  When some
+// |scale| >= 64 (big, wave-uniform) -1024 s overflows fp16; then x - 1024 is
+// formed first (exact) and the addend is 0.  The adjustment is a branch
+// inside the same instruction stream, so both cases share registers.
+template <int HD>
 __device__ inline void pv_group(WaveState<HD>& st, half8_t pa, const uint32_t* vc, u32x4 vs4,
-                                const Nibble& nb) {
+                                const Nibble& nb, bool big) {
   constexpr int CPL = HD / 16;
   const half8_t sv = as_h8(vs4);
   const half8_t inv16 = {(_Float16)0.0625f, (_Float16)0.0625f, (_Float16)0.0625f,
                          (_Float16)0.0625f, (_Float16)0.0625f, (_Float16)0.0625f,
                          (_Float16)0.0625f, (_Float16)0.0625f};
-  const half8_t m1024 = {(_Float16)-1024.f, (_Float16)-1024.f, (_Float16)-1024.f,
-                         (_Float16)-1024.f, (_Float16)-1024.f, (_Float16)-1024.f,
-                         (_Float16)-1024.f, (_Float16)-1024.f};
+  const _Float16 off = big ? (_Float16)0.0f : (_Float16)-1024.f;
+  const half8_t offv = {off, off, off, off, off, off, off, off};
   const u32x4 s_lo = vs4;
-  const u32x4 s_hi = as_u4(sv * inv16);
-  u32x4 n_lo = {0u, 0u, 0u, 0u}, n_hi = {0u, 0u, 0u, 0u};
-  if constexpr (!kBig) {
-    n_lo = as_u4(sv * m1024);           // -1024 s, exact
-    n_hi = as_u4(as_h8(s_hi) * m1024);  // -64 s, exact
-  }
+  const half8_t shi = sv * inv16;
+  const u32x4 s_hi = as_u4(shi);
+  const u32x4 n_lo = as_u4(sv * offv);   // -1024 s (exact) or 0
+  const u32x4 n_hi = as_u4(shi * offv);  // -64 s (exact) or 0
   const half2_t m1024_2 = {(_Float16)-1024.f, (_Float16)-1024.f};
 #pragma unroll
   for (int k = 0; k < CPL / 2; ++k) {
-    u32x4 lo, hi;
+    uint32_t xl[4], xh[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const uint32_t y = __builtin_amdgcn_perm(vc[2 * q + 1], vc[2 * q], nb.sel[k]);
-      const uint32_t xl = (y & nb.lo) | nb.magic;  // (1024 + c, 1024 + c')
-      const uint32_t xh = (y & nb.hi) | nb.magic;  // (1024 + 16c, 1024 + 16c')
-      if constexpr (!kBig) {
-        lo[q] = as_u(__builtin_elementwise_fma(as_h2(xl), as_h2(s_lo[q]), as_h2(n_lo[q])));
-        hi[q] = as_u(__builtin_elementwise_fma(as_h2(xh), as_h2(s_hi[q]), as_h2(n_hi[q])));
-      } else {
-        lo[q] = as_u((as_h2(xl) + m1024_2) * as_h2(s_lo[q]));
-        hi[q] = as_u((as_h2(xh) + m1024_2) * as_h2(s_hi[q]));
+      xl[q] = (y & nb.lo) | nb.magic;  // (1024 + c, 1024 + c')
+      xh[q] = (y & nb.hi) | nb.magic;  // (1024 + 16c, 1024 + 16c')
+    }
+    if (__builtin_expect(big, 0)) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        xl[q] = as_u(as_h2(xl[q]) + m1024_2);
+        xh[q] = as_u(as_h2(xh[q]) + m1024_2);
       }
+    }
+    u32x4 lo, hi;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      lo[q] = as_u(__builtin_elementwise_fma(as_h2(xl[q]), as_h2(s_lo[q]), as_h2(n_lo[q])));
+      hi[q] = as_u(__builtin_elementwise_fma(as_h2(xh[q]), as_h2(s_hi[q]), as_h2(n_hi[q])));
     }
     st.o[2 * k] = mfma(pa, as_h8(lo), st.o[2 * k]);
     st.o[2 * k + 1] = mfma(pa, as_h8(hi), st.o[2 * k + 1]);
@@ -309,62 +445,44 @@ struct SegCtx {
   half8_t qp[HD / 32];  // B operand of Q in the unpack order, odd channels / 16
 };
 
-// One quantised 32-token group: QK^T, online softmax, PV.
+// One quantised 32-token group (already in LDS): QK^T, online softmax, PV.
 template <int HD, int P>
-__device__ inline void group_compute(WaveState<HD>& st, const SegCtx<HD>& q, const Stage<HD, P>& cur,
-                                     const CodeBuf<HD>* buf, uint16_t (*ksz_s)[HD],
-                                     uint16_t (*vsz_s)[HD / kGroup][kGroup], const LaneMap& lm,
-                                     const Nibble& nb, float sscale, int lane) {
+__device__ inline void group_compute(WaveState<HD>& st, const SegCtx<HD>& q,
+                                     const StageBuf<HD>* buf, const LaneMap& lm, const Nibble& nb,
+                                     float sscale, int lane) {
   using C = Cfg<HD, P>;
-  constexpr int KS = C::KS, CPL = C::CPL, HDG = C::HDG;
-  const int c = lane & 15, j = lane >> 4, which = lane >> 5, t32 = lane & 31;
+  constexpr int KS = C::KS, CPL = C::CPL;
+  const int c = lane & 15, j = lane >> 4;
   const half8_t neg1024 = {(_Float16)-1024.f, (_Float16)-1024.f, (_Float16)-1024.f,
                            (_Float16)-1024.f, (_Float16)-1024.f, (_Float16)-1024.f,
                            (_Float16)-1024.f, (_Float16)-1024.f};
-  // scales / zeros through LDS into the operand layouts
-  *(typename C::pvec*)&ksz_s[which][lm.ksoff] = cur.ksz;
-  if constexpr (HDG == 4) {
-    vsz_s[which][0][t32] = (uint16_t)cur.vsz[0];
-    vsz_s[which][1][t32] = (uint16_t)(cur.vsz[0] >> 16);
-    vsz_s[which][2][t32] = (uint16_t)cur.vsz[1];
-    vsz_s[which][3][t32] = (uint16_t)(cur.vsz[1] >> 16);
-  } else {
-    vsz_s[which][0][t32] = (uint16_t)cur.vsz;
-    vsz_s[which][1][t32] = (uint16_t)(cur.vsz >> 16);
-  }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
-  __builtin_amdgcn_wave_barrier();
   typename C::kvec kc[2];
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    if constexpr (HD == 128) {
-      kc[tt] = *(const u32x4*)&buf->k[tt][16 * lane];
-    } else {
-      kc[tt][0] = *(const uint32_t*)&buf->k[tt][4 * lane];
-      kc[tt][1] = *(const uint32_t*)&buf->k[tt][256 + 4 * lane];
-    }
-  }
-  uint32_t vc[8];
+  for (int tt = 0; tt < 2; ++tt) kc[tt] = *(const typename C::kvec*)&buf->k[lm.kread[tt]];
+  uint32_t vc[8];  // row tok_v(j, e)
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
+  for (int e = 0; e < 8; ++e) {
+    const uint8_t* vp = &buf->v[lm.vread + 2 * e * C::HDP];
     if constexpr (CPL == 8)
-      vc[r] = *(const uint32_t*)&buf->v[r][4 * lane];
+      vc[e] = *(const uint32_t*)vp;
     else
-      vc[r] = *(const uint16_t*)&buf->v[r][4 * lane];
+      vc[e] = *(const uint16_t*)vp;
   }
 
   // ---- S^T = K Q^T; B = q*s as fp16 hi + lo (lo = fma(q, s, -hi)) ----
-  floatx4 bias = {0.f, 0.f, 0.f, 0.f}, s0 = bias, s1 = bias;
+  // three independent bias chains keep the dependent-MFMA latency short
+  floatx4 bz = {0.f, 0.f, 0.f, 0.f}, bh = bz, bl = bz, s0 = bz, s1 = bz;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    const u32x4 sv = *(const u32x4*)&ksz_s[0][j * (HD / 4) + 8 * ks];
-    const u32x4 zv = *(const u32x4*)&ksz_s[1][j * (HD / 4) + 8 * ks];
+    const uint8_t* kp = &buf->s[2 * (j * (HD / 4) + 8 * ks)];
+    const u32x4 sv = *(const u32x4*)kp;
+    const u32x4 zv = *(const u32x4*)(kp + 2 * HD);
     const half8_t sp = as_h8(perm_pairs(sv));
     const half8_t qs = q.qp[ks] * sp;
     const half8_t ql = __builtin_elementwise_fma(q.qp[ks], sp, -qs);
-    bias = mfma(as_h8(zv), q.qn[ks], bias);  // sum_d z_d q_gd
-    bias = mfma(neg1024, qs, bias);           // -1024 sum_d B_gd
-    bias = mfma(neg1024, ql, bias);
+    bz = mfma(as_h8(zv), q.qn[ks], bz);  // sum_d z_d q_gd
+    bh = mfma(neg1024, qs, bh);           // -1024 sum_d B_gd
+    bl = mfma(neg1024, ql, bl);
     const half8_t x0 = as_h8(unpack_codes(kc[0][ks], nb));
     const half8_t x1 = as_h8(unpack_codes(kc[1][ks], nb));
     s0 = mfma(x0, qs, s0);
@@ -373,27 +491,37 @@ __device__ inline void group_compute(WaveState<HD>& st, const SegCtx<HD>& q, con
     s1 = mfma(x1, ql, s1);
   }
   // every row of the bias tile holds the same per-head constant
-  const half8_t pa = softmax_tile<HD>(st, s0, s1, sscale, bias[0] * sscale, j);
+  const float bias = bz[0] + (bh[0] + bl[0]);
+  const half8_t pa = softmax_tile<HD>(st, s0, s1, sscale, bias * sscale, j);
 
   // ---- V dequant (packed fp16) and PV ----
-  const int vg = (CPL * c) / kGroup;
-  const u32x4 vs4 = *(const u32x4*)&vsz_s[0][vg][8 * j];
-  const u32x4 vz4 = *(const u32x4*)&vsz_s[1][vg][8 * j];
+  // pair q: tokens tok_v(j, 2q) and tok_v(j, 2q + 1), two rows apart
+  constexpr int HDG = C::HDG;
+  const uint8_t* vp = &buf->s[4 * HD + lm.vsread];
+  u32x4 vs4, vz4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint8_t* p0 = vp + 8 * HDG * e;
+    vs4[e] = (uint32_t)*(const uint16_t*)p0 | ((uint32_t)*(const uint16_t*)(p0 + 4 * HDG) << 16);
+    vz4[e] = (uint32_t)*(const uint16_t*)(p0 + 64 * HDG) |
+             ((uint32_t)*(const uint16_t*)(p0 + 64 * HDG + 4 * HDG) << 16);
+  }
   st.ob = mfma(pa, as_h8(vz4), st.ob);
-  const bool small =
-      small_pair(vs4[0]) && small_pair(vs4[1]) && small_pair(vs4[2]) && small_pair(vs4[3]);
-  if (__builtin_amdgcn_ballot_w64(!small) == 0)
-    pv_group<HD, false>(st, pa, vc, vs4, nb);
-  else
-    pv_group<HD, true>(st, pa, vc, vs4, nb);
-  __builtin_amdgcn_wave_barrier();  // LDS reads above precede the next group's writes
+  // |s| >= 64 is fp16 exponent field >= 0x15; the OR of the bit patterns
+  // reaches it whenever one value does (and, rarely, when none does, which
+  // only selects the exact-but-slower arithmetic)
+  const uint32_t sor = (vs4[0] | vs4[1] | vs4[2] | vs4[3]) & 0x7FFF7FFFu;
+  const bool big = (sor & 0xFFFFu) >= 0x5400u || sor >= 0x54000000u;
+  pv_group<HD>(st, pa, vc, vs4, nb, __builtin_amdgcn_ballot_w64(big) != 0);
 }
 
 // Tiles of one sequence: 32-token tiles of its decode window, at least one so
 // that an empty sequence still produces its (zero) output.
 __device__ inline int seq_tiles(const KiviGeo& g, const DecodeArgs& a, int b, int* ov, int* n) {
   int o, r;
-  decode_window(g, a.seq_lens ? a.seq_lens[b] : a.seq_len, &o, &r);
+  decode_window(g, a.seq_lens ? ((const __attribute__((address_space(4))) int32_t*)a.seq_lens)[b]
+                              : a.seq_len,
+                &o, &r);
   *ov = o;
   *n = o + r;
   return max(1, (o + r + kGroup - 1) / kGroup);
@@ -420,7 +548,7 @@ __device__ inline int64_t stream_tiles(const KiviGeo& g, const DecodeArgs& a, in
   for (int base = 0; base < a.batch; base += 64) {
     int T = 0, ov, n;
     if (base + lane < a.batch) T = seq_tiles(g, a, base + lane, &ov, &n);
-    tot += wave_sum_i(T);
+    tot += __builtin_amdgcn_readfirstlane(wave_sum_i(T));
   }
   return tot * g.nkv;
 }
@@ -452,10 +580,10 @@ __device__ inline SeqSpan locate(const KiviGeo& g, const DecodeArgs& a, int64_t 
     const uint64_t hit = __builtin_amdgcn_ballot_w64(bb < a.batch && run + (int64_t)g.nkv * incl > x);
     if (hit) {
       const int f = __builtin_ctzll(hit);
-      const int Tf = __shfl(T, f, 64), If = __shfl(incl, f, 64);
+      const int Tf = __builtin_amdgcn_readlane(T, f), If = __builtin_amdgcn_readlane(incl, f);
       return {base + f, run + (int64_t)g.nkv * (If - Tf), Tf};
     }
-    run += (int64_t)g.nkv * __shfl(incl, 63, 64);
+    run += (int64_t)g.nkv * __builtin_amdgcn_readlane(incl, 63);
   }
   return {a.batch, run, 1};
 }
@@ -464,10 +592,8 @@ template <int HD, int P>
 __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, DecodeArgs a) {
   using C = Cfg<HD, P>;
   constexpr int KS = C::KS, CPL = C::CPL;
-  __shared__ __attribute__((aligned(16))) uint16_t ksz_s[2][HD];
-  __shared__ __attribute__((aligned(16))) uint16_t vsz_s[2][C::HDG][kGroup];
-  __shared__ __attribute__((aligned(16))) CodeBuf<HD> bufA;
-  __shared__ __attribute__((aligned(16))) CodeBuf<HD> bufB;
+  constexpr int L = stage_loads<HD>(), S = kStages;
+  __shared__ __attribute__((aligned(16))) StageBuf<HD> ring[S];
 
   const int lane = threadIdx.x, c = lane & 15, j = lane >> 4;
   const int G = g.gqa, NKV = g.nkv;
@@ -481,7 +607,7 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
   const Nibble nb;
   const LaneMap lm = lane_map<HD, P>(lane);
   const float sscale = 1.4426950408889634f / __builtin_sqrtf((float)HD);  // log2(e)/sqrt(HD)
-  const int which = lane >> 5;
+  const int which = lane >> 5, t32 = lane & 31;
 
   SeqSpan sp = locate(g, a, x0, lane);
   int kvh = (int)((x0 - sp.start) / sp.tiles);
@@ -513,46 +639,43 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
     st.m = -1.0e30f;
     st.l = 0.0f;
 
-    // ---- quantised groups, two stages in flight ----
+    // ---- quantised groups: a ring of S LDS stages, S - 1 in flight ----
     const int tq_end = min(t_fin, ov / kGroup);
     if (t_beg < tq_end) {
-      const int32_t* bt = a.block_tables + (int64_t)b * a.bt_stride;
-      StageBases sb;
-      sb.code_page = (uint32_t)(NKV * P * C::HDP);
-      sb.vsz_page = (uint32_t)(NKV * P * C::HDG);
-      sb.ksz_page = (uint32_t)(NKV * HD);
-      sb.kcode = a.k_code + (int64_t)h * P * C::HDP;
-      sb.vcode = a.v_code + (int64_t)h * P * C::HDP;
-      sb.ksz = (which ? a.k_zero : a.k_scale) + (int64_t)h * HD;
-      sb.vsz = (which ? a.v_zero : a.v_scale) + (int64_t)h * P * C::HDG;
+      // read-only for the whole launch: the constant address space lets the
+      // wave-uniform page reads be scalar loads (lgkmcnt, not vmcnt)
+      const __attribute__((address_space(4))) int32_t* bt =
+          (const __attribute__((address_space(4))) int32_t*)(a.block_tables +
+                                                             (int64_t)b * a.bt_stride);
+      const StageBases sb = stage_bases<HD, P>(a, NKV, h, lane);
       auto page = [&](int tile, int k) -> uint32_t {
         return (uint32_t)bt[tile * C::PPG + (C::PPG == 2 ? k : 0)];
       };
-      Stage<HD, P> A, B;
-      load_stage<HD, P>(A, &bufA, sb, lm, page(t_beg, 0), page(t_beg, 1));
-      uint32_t n0 = 0, n1 = 0;  // pages of the next group to load
-      if (t_beg + 1 < tq_end) {
-        n0 = page(t_beg + 1, 0);
-        n1 = page(t_beg + 1, 1);
+      wait_vm<0>();  // the counts below see only this loop's DMAs
+#pragma unroll
+      for (int k = 0; k < S - 1; ++k)
+        if (t_beg + k < tq_end)
+          load_stage<HD, P>(&ring[k], sb, page(t_beg + k, 0), page(t_beg + k, 1), lane);
+      uint32_t n0 = 0, n1 = 0;  // pages of group i + S - 1, read one group early
+      if (t_beg + S - 1 < tq_end) {
+        n0 = page(t_beg + S - 1, 0);
+        n1 = page(t_beg + S - 1, 1);
       }
-      for (int i = t_beg; i < tq_end; i += 2) {
-        if (i + 1 < tq_end) {
-          load_stage<HD, P>(B, &bufB, sb, lm, n0, n1);
-          if (i + 2 < tq_end) {
-            n0 = page(i + 2, 0);
-            n1 = page(i + 2, 1);
+      int slot = 0;
+      for (int i = t_beg; i < tq_end; ++i) {
+        const int ahead = slot == 0 ? S - 1 : slot - 1;  // (slot + S - 1) % S
+        if (i + S - 1 < tq_end) {
+          load_stage<HD, P>(&ring[ahead], sb, n0, n1, lane);
+          if (i + S < tq_end) {
+            n0 = page(i + S, 0);
+            n1 = page(i + S, 1);
           }
+          wait_vm<(S - 1) * L>();
+        } else {
+          wait_stages<L, S>(tq_end - 1 - i);
         }
-        group_compute<HD, P>(st, q, A, &bufA, ksz_s, vsz_s, lm, nb, sscale, lane);
-        if (i + 1 >= tq_end) break;
-        if (i + 2 < tq_end) {
-          load_stage<HD, P>(A, &bufA, sb, lm, n0, n1);
-          if (i + 3 < tq_end) {
-            n0 = page(i + 3, 0);
-            n1 = page(i + 3, 1);
-          }
-        }
-        group_compute<HD, P>(st, q, B, &bufB, ksz_s, vsz_s, lm, nb, sscale, lane);
+        group_compute<HD, P>(st, q, &ring[slot], lm, nb, sscale, lane);
+        slot = slot == S - 1 ? 0 : slot + 1;
       }
     }
 
@@ -563,42 +686,45 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
       const int t0 = i * kGroup;
       const int tn = min(kGroup, n - t0);  // 0 only for an empty sequence
       const int r0 = t0 - ov;              // scratch row of token t0
-      floatx4 s[2];
+      // every load is issued before the first use (rows past the end read
+      // row r0, a valid scratch row, and are masked afterwards)
+      u32x4 kv[2][KS];
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         const int tl = 8 * (c >> 2) + 4 * tt + (c & 3);
+        const uint16_t* kr = kscr + (int64_t)(r0 + (tl < tn ? tl : 0)) * HD + j * (HD / 4);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) kv[tt][ks] = __builtin_nontemporal_load((const u32x4*)(kr + 8 * ks));
+      }
+      typedef typename std::conditional<CPL == 8, u32x4, u32x2>::type vrow_t;
+      vrow_t vr[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int tl = 8 * j + r;
+        vr[r] = __builtin_nontemporal_load(
+            (const vrow_t*)(vscr + (int64_t)(r0 + (tl < tn ? tl : 0)) * HD + CPL * c));
+      }
+      floatx4 s[2];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
         s[tt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          u32x4 kv = {0u, 0u, 0u, 0u};
-          if (tl < tn)
-            kv = *(const u32x4*)(kscr + (int64_t)(r0 + tl) * HD + j * (HD / 4) + 8 * ks);
-          s[tt] = mfma(as_h8(kv), q.qn[ks], s[tt]);
-        }
+        for (int ks = 0; ks < KS; ++ks) s[tt] = mfma(as_h8(kv[tt][ks]), q.qn[ks], s[tt]);
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii)
           if (8 * j + 4 * tt + ii >= tn) s[tt][ii] = -INFINITY;
       }
       const half8_t pa = softmax_tile<HD>(st, s[0], s[1], sscale, 0.0f, j);
-      // V rows 8j..8j+7, channels CPL*c.. : fp16 values straight from scratch
-      uint32_t vr[8][CPL / 2];
+      // rows past the end carry P = 0 but must not carry NaN/Inf garbage
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const int tl = 8 * j + r;
-#pragma unroll
-        for (int wd = 0; wd < CPL / 2; ++wd) vr[r][wd] = 0u;
-        if (tl < tn) {
-          const uint32_t* src = (const uint32_t*)(vscr + (int64_t)(r0 + tl) * HD + CPL * c);
-#pragma unroll
-          for (int wd = 0; wd < CPL / 2; ++wd) vr[r][wd] = src[wd];
-        }
-      }
+      for (int r = 0; r < 8; ++r)
+        if (8 * j + r >= tn) vr[r] = vrow_t(0u);
 #pragma unroll
       for (int nt = 0; nt < CPL; ++nt) {
         u32x4 vb;
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
-          const uint32_t va = vr[2 * qq][nt >> 1], vb2 = vr[2 * qq + 1][nt >> 1];
+          const uint32_t va = vr[2 * qq][nt >> 1], vb2 = vr[2 * qq + 1][nt >> 1];  // rows 2qq, 2qq+1
           vb[qq] = (nt & 1) ? __builtin_amdgcn_perm(vb2, va, 0x07060302u)
                             : __builtin_amdgcn_perm(vb2, va, 0x05040100u);
         }
