@@ -153,9 +153,11 @@ size_t partial_slots(const KiviGeo& g, int batch, const SplitPlan& sp, int waves
   return (size_t)batch * g.nkv + (size_t)waves;
 }
 
-// Workspace: [m,l fp32 per slot and head][acc fp32 per slot, head, channel].
+// Workspace: [m,l fp32 per slot and head][acc fp32 per slot, head, channel]
+// and, for the matrix-core kernel, [first, last wavefront int32 per segment].
 size_t workspace_bytes(const KiviGeo& g, int batch, const SplitPlan& sp, int waves) {
-  return partial_slots(g, batch, sp, waves) * g.gqa * (size_t)(g.hd + 2) * sizeof(float);
+  const size_t seg = use_simple_decode() ? 0 : (size_t)batch * g.nkv * 2 * sizeof(int32_t);
+  return partial_slots(g, batch, sp, waves) * g.gqa * (size_t)(g.hd + 2) * sizeof(float) + seg;
 }
 
 void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& sp, int waves,
@@ -166,6 +168,7 @@ void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& 
   const size_t slots = partial_slots(g, batch, sp, waves) * g.gqa;
   a.ws_ml = (float*)ws;
   a.ws_acc = ws ? a.ws_ml + slots * 2 : nullptr;
+  a.ws_seg = ws ? (int32_t*)(a.ws_acc + slots * g.hd) : nullptr;
 }
 
 // Decode with a runtime geometry; seq_len_host >= 0 when the (single) length
@@ -186,7 +189,7 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
     max_tokens = ov + rv;
   }
   const SplitPlan sp = plan_splits(max_tokens);
-  const int waves = jacq::decode_stream_waves(g_dev[dev].cus);
+  const int waves = jacq::decode_stream_waves(g, g_dev[dev].cus);
   const size_t need = workspace_bytes(g, batch, sp, waves);
   if (need > 0) {
     if (ws == nullptr) {
@@ -299,7 +302,7 @@ size_t jacq_kivi_decode_workspace_size(const jacq_kivi_geometry* geo, int32_t ba
   if (current_device(&dev) != JACQ_KIVI_OK) return 0;
   const KiviGeo g = make_geo(*geo);
   return workspace_bytes(g, batch, plan_splits(max_seq_len(*geo)),
-                         jacq::decode_stream_waves(g_dev[dev].cus));
+                         jacq::decode_stream_waves(g, g_dev[dev].cus));
 }
 
 int jacq_kivi_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q, const int32_t* SEQ_LENS,

@@ -763,6 +763,11 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
       a.ws_ml[(piece * G + c) * 2] = st.m;
       a.ws_ml[(piece * G + c) * 2 + 1] = lsum;
     }
+    if (lane == 0) {  // the combine kernel's map: first and last wavefront of the segment
+      const int64_t seg = (int64_t)b * NKV + h;
+      if (t_beg == 0) a.ws_seg[2 * seg] = w;
+      if (t_fin == T) a.ws_seg[2 * seg + 1] = w;
+    }
 
     x += t_fin - t_beg;
     t = 0;
@@ -776,58 +781,53 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
 // Log-sum-exp merge of the partials of one (sequence, kv head) left by the
 // wavefronts whose runs cut it (variants.rs:3548-3565).  One workgroup per
 // (kv head, sequence); a separate launch, so every partial is visible across
-// the GPU's L2 slices without device-scope fences in the decode kernel.
+// the GPU's L2 slices without device-scope fences in the decode kernel.  The
+// decode kernel records the first and last wavefront of every segment, so a
+// segment that one wavefront finished costs a single scalar load here, and a
+// cut one loads all of its partials at once.
 __global__ __launch_bounds__(256) void kivi_combine_stream_kernel(KiviGeo g, DecodeArgs a) {
-  __shared__ int64_t span_s[3];  // tiles before sequence b (x NKV), total tiles, T_b
-  __shared__ float inv_s[16], mx_s[16];
+  constexpr int K = 8;  // outputs per thread: G * HD <= 16 * 128
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int G = g.gqa, HD = g.hd, NKV = g.nkv;
-  if (tid < 64) {
-    const int64_t TT = stream_tiles(g, a, tid);
-    int64_t before = 0;
-    for (int base = 0; base < b; base += 64) {
-      int T = 0, ov, n;
-      if (base + tid < b) T = seq_tiles(g, a, base + tid, &ov, &n);
-      before += wave_sum_i(T);
-    }
-    int ov, n;
-    const int Tb = seq_tiles(g, a, b, &ov, &n);
-    if (tid == 0) {
-      span_s[0] = before * NKV;
-      span_s[1] = TT;
-      span_s[2] = Tb;
-    }
-  }
-  __syncthreads();
-  const int64_t TT = span_s[1], Tb = span_s[2];
-  const int64_t W = stream_waves(TT, a.waves);
-  const int64_t s = span_s[0] + (int64_t)h * Tb, e = s + Tb;
-  auto wave_of = [&](int64_t x) -> int64_t { return ((x + 1) * W - 1) / TT; };
-  const int64_t w0 = wave_of(s), w1 = wave_of(e - 1);
-  if (w0 == w1) return;  // one wavefront covered it and wrote O
+  const int G = g.gqa, HD = g.hd, NKV = g.nkv, n = G * HD;
   const int64_t seg = (int64_t)b * NKV + h;
-  if (tid < G) {
-    float M = -INFINITY;
-    for (int64_t w = w0; w <= w1; ++w) M = fmaxf(M, a.ws_ml[((seg + w) * G + tid) * 2]);
-    float L = 0.f;
-    for (int64_t w = w0; w <= w1; ++w) {
-      const int64_t p = (seg + w) * G + tid;
-      L += a.ws_ml[p * 2 + 1] * __builtin_amdgcn_exp2f(a.ws_ml[p * 2] - M);
-    }
-    mx_s[tid] = M;
-    inv_s[tid] = 1.0f / fmaxf(L, 1.0e-30f);
+  const __attribute__((address_space(4))) int32_t* sw =
+      (const __attribute__((address_space(4))) int32_t*)a.ws_seg;
+  const int w0 = sw[2 * seg], w1 = sw[2 * seg + 1];
+  if (w0 >= w1) return;  // written whole by the decode kernel
+  int gi[K], d[K];
+  float M[K], L[K], acc[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int e = min(tid + 256 * k, n - 1);
+    gi[k] = e / HD;
+    d[k] = e - gi[k] * HD;
+    M[k] = -INFINITY;
+    L[k] = 0.0f;
+    acc[k] = 0.0f;
   }
-  __syncthreads();
-  for (int e2 = tid; e2 < G * HD; e2 += 256) {
-    const int gi = e2 / HD, d = e2 % HD;
-    const float M = mx_s[gi];
-    float acc = 0.f;
-    for (int64_t w = w0; w <= w1; ++w) {
-      const int64_t p = (seg + w) * G + gi;
-      acc += a.ws_acc[p * HD + d] * __builtin_amdgcn_exp2f(a.ws_ml[p * 2] - M);
+  // every load of one partial is issued before the first is used
+  for (int w = w0; w <= w1; ++w) {
+    float m[K], l[K], v[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int64_t p = (seg + w) * G + gi[k];
+      m[k] = a.ws_ml[2 * p];
+      l[k] = a.ws_ml[2 * p + 1];
+      v[k] = a.ws_acc[p * HD + d[k]];
     }
-    a.out[(int64_t)b * a.out_stride + ((int64_t)h * G + gi) * HD + d] = acc * inv_s[gi];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float mn = fmaxf(M[k], m[k]);
+      const float fo = __builtin_amdgcn_exp2f(M[k] - mn), fn = __builtin_amdgcn_exp2f(m[k] - mn);
+      acc[k] = acc[k] * fo + v[k] * fn;
+      L[k] = L[k] * fo + l[k] * fn;
+      M[k] = mn;
+    }
   }
+  float* out = a.out + (int64_t)b * a.out_stride + (int64_t)h * G * HD;
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    if (tid + 256 * k < n) out[(int64_t)gi[k] * HD + d[k]] = acc[k] / fmaxf(L[k], 1.0e-30f);
 }
 
 template <int HD, int P>
@@ -851,6 +851,34 @@ hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
   return hipGetLastError();
 }
 
-int decode_stream_waves(int cus) { return cus * 8; }
+// One resident wavefront per slot: the tile stream is cut into as many runs as
+// the device holds waves of this kernel at once (registers and LDS decide how
+// many fit on a CU), so no CU idles and none runs a second round.
+template <int HD, int P>
+static int resident_per_cu() {
+  static int n = 0;
+  if (n == 0) {
+    int k = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, kivi_decode_stream_kernel<HD, P>, 64, 0) !=
+            hipSuccess ||
+        k < 1)
+      k = 8;
+    n = k;
+  }
+  return n;
+}
+
+int decode_stream_waves(const KiviGeo& g, int cus) {
+  int per = 8;
+  if (g.hd == 128 && g.page == 16)
+    per = resident_per_cu<128, 16>();
+  else if (g.hd == 128)
+    per = resident_per_cu<128, 32>();
+  else if (g.page == 16)
+    per = resident_per_cu<64, 16>();
+  else
+    per = resident_per_cu<64, 32>();
+  return cus * per;
+}
 
 }  // namespace jacq

@@ -45,6 +45,7 @@ struct DecodeArgs {
   int64_t out_stride;
   float* ws_ml;   // [batch, NKV, max_splits, G, 2]  (m, l)
   float* ws_acc;  // [batch, NKV, max_splits, G, HD]
+  int32_t* ws_seg;  // matrix-core kernel: [batch, NKV, 2] first / last wavefront of a segment
   int max_splits;  // VALU kernel: split slots per (sequence, kv head)
   int batch;       // sequences (queries) in the call
   int waves;       // matrix-core kernel: wavefronts sharing the tile stream
@@ -54,7 +55,8 @@ hipError_t launch_append(const KiviGeo& g, const AppendArgs& a, int batch, hipSt
 hipError_t launch_decode(const KiviGeo& g, const DecodeArgs& a, int batch, hipStream_t stream);
 hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
                               hipStream_t stream);
-// wavefronts the matrix-core decode launches on a device with `cus` CUs
-int decode_stream_waves(int cus);
+// wavefronts the matrix-core decode launches on a device with `cus` CUs:
+// as many as are resident at once
+int decode_stream_waves(const KiviGeo& g, int cus);
 
 }  // namespace jacq
