@@ -12,8 +12,10 @@ stream the kernels run on; a 512 MiB buffer is written before every step so
 the 256 MiB MALL and the L2 start cold.
 
 Prints ONE JSON line.  `value` is the effective KV bandwidth of the decode
-(algorithmic bytes / decode time, GB/s); `ms_per_step` is the decode time per
-step.  The CPU baseline runs the oracle (oracle/, a C restatement of the
+(algorithmic bytes / decode time, GB/s, both decode launches: the main kernel
+and the split-K merge); `ms_per_step` is that decode time per step.
+`roofline.achieved` is the same bytes over the main kernel alone, timed with
+HIP events the library records on the launch stream (jacq_kivi_profile_*).  The CPU baseline runs the oracle (oracle/, a C restatement of the
 reference path) over the same state on this host's cores.
 """
 from __future__ import annotations
@@ -42,6 +44,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-flush", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="instead of the workload, copy MIB MiB device-to-device a few times "
+                         "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -63,6 +68,8 @@ def main() -> int:
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        return copy_calibration(torch, dev, args.copy_calibration)
     w = wl.WORKLOADS[args.workload]
     rng = np.random.default_rng(w.seed)
     lens0 = wl.context_lens(w, rng)            # lengths when timing starts (after prefill)
@@ -117,6 +124,7 @@ def main() -> int:
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(total_steps)]
     stream = torch.cuda.current_stream(dev)
     torch.cuda.synchronize()
+    kivi.profile_start(total_steps)  # events around the decode kernel itself
     wall0 = None
     for i in range(total_steps):
         if i == args.warmup:
@@ -134,6 +142,9 @@ def main() -> int:
         lens_after.add_(1)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
+    kern_ms, merge_ms = kivi.profile_stop(total_steps)
+    kern = np.array(kern_ms[args.warmup:])
+    merge = np.array(merge_ms[args.warmup:])
 
     dec_ms, wr_ms, step_bytes = [], [], []
     for i in range(args.warmup, total_steps):
@@ -145,6 +156,7 @@ def main() -> int:
     dec = np.array(dec_ms)
     wr = np.array(wr_ms)
     gbs = float(np.sum(step_bytes) / (dec.sum() * 1e-3) / 1e9)
+    kern_gbs = float(np.sum(step_bytes) / (kern.sum() * 1e-3) / 1e9)
     bytes_per_step = float(np.mean(step_bytes))
 
     # ---- CPU baseline: the oracle over the same final state on this host ----
@@ -165,7 +177,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": "int4 KV, fp16 MFMA operands, fp32 accumulate",
         "data": "synthetic",
         "config": {
             "workload": f"{w.name}: {w.nh}q/{w.nkv}kv heads, head_dim {w.hd}, batch {B}, "
@@ -180,6 +192,10 @@ def main() -> int:
                       "min": round(float(dec.min()) * 1e3, 2),
                       "median": round(float(np.median(dec)) * 1e3, 2),
                       "p90": round(float(np.percentile(dec, 90)) * 1e3, 2)},
+        "kernel_us": {"mean": round(float(kern.mean()) * 1e3, 2),
+                      "median": round(float(np.median(kern)) * 1e3, 2),
+                      "min": round(float(kern.min()) * 1e3, 2)},
+        "merge_us": {"mean": round(float(merge.mean()) * 1e3, 2)},
         "write_us": {"mean": round(float(wr.mean()) * 1e3, 2),
                      "median": round(float(np.median(wr)) * 1e3, 2)},
         "step_us_write_plus_decode": round(float((dec + wr).mean()) * 1e3, 2),
@@ -187,11 +203,12 @@ def main() -> int:
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "wall_s_timed_region": round(wall, 4),
         "roofline": {
+            "kernel": "kivi_decode_stream_kernel",
             "bound": "hbm",
-            "achieved": round(gbs, 1),
+            "achieved": round(kern_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
         },
         "cpu_baseline": cpu,
@@ -199,6 +216,19 @@ def main() -> int:
     if prefill_info:
         line["prefill_write"] = prefill_info
     print(json.dumps(line), flush=True)
+    return 0
+
+
+def copy_calibration(torch, dev, mib: int) -> int:
+    """A plain device copy of known size: its FETCH_SIZE / WRITE_SIZE under
+    rocprofv3 --pmc give the counters' bytes-per-unit on this GPU."""
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty(n, dtype=torch.uint8, device=dev)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "copies": 3}), flush=True)
     return 0
 
 

@@ -245,6 +245,16 @@ typedef struct jacq_kivi_subchunk {
 int32_t jacq_kivi_plan_batched_write(int32_t start_seq_len, int32_t num_new, int32_t residual,
                                      int32_t group, jacq_kivi_subchunk* out, int32_t cap);
 
+/* Measurement hook (no counterpart in the reference; for benchmarks and
+ * profilers).  jacq_kivi_profile_start enables recording for the next
+ * max_calls decode calls: each records HIP events on its own stream around
+ * its main kernel and its split-K merge.  jacq_kivi_profile_stop disables
+ * recording, waits for the events and writes the per-call milliseconds of
+ * the main kernel and of the merge (at most cap entries); it returns the
+ * number of calls written or -1. */
+int jacq_kivi_profile_start(int32_t max_calls);
+int32_t jacq_kivi_profile_stop(float* kernel_ms, float* merge_ms, int32_t cap);
+
 #ifdef __cplusplus
 }
 #endif

@@ -171,6 +171,25 @@ void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& 
   a.ws_seg = ws ? (int32_t*)(a.ws_acc + slots * g.hd) : nullptr;
 }
 
+// ---- measurement hook: HIP events around the two decode launches ----
+// While enabled, each decode call takes the next triple of a pre-created
+// event pool and records it on the call's own stream: before the main
+// kernel, between it and the split-K merge, and after the merge.
+struct Profiler {
+  bool on = false;
+  int used = 0;
+  std::vector<hipEvent_t> ev;  // 3 per call
+};
+std::mutex g_prof_mu;
+Profiler g_prof;
+
+void profile_slot(hipEvent_t out[3]) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  if (!g_prof.on || 3 * (g_prof.used + 1) > (int)g_prof.ev.size()) return;
+  for (int i = 0; i < 3; ++i) out[i] = g_prof.ev[3 * g_prof.used + i];
+  ++g_prof.used;
+}
+
 // Decode with a runtime geometry; seq_len_host >= 0 when the (single) length
 // is known on the host, which tightens the split plan.
 int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t* seq_lens,
@@ -219,9 +238,16 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
   a.out = O;
   a.out_stride = (int64_t)g.nh * g.hd;
   fill_ws(a, g, batch, sp, waves, need > 0 ? ws : nullptr);
-  const hipError_t e = use_simple_decode() ? jacq::launch_decode(g, a, batch, stream)
-                                            : jacq::launch_decode_mfma(g, a, batch, stream);
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+  profile_slot(ev);
+  if (ev[0] && hipEventRecord(ev[0], stream) != hipSuccess)
+    return fail(JACQ_KIVI_EHIP, "hipEventRecord failed");
+  const hipError_t e = use_simple_decode()
+                           ? jacq::launch_decode(g, a, batch, stream, ev[1])
+                           : jacq::launch_decode_mfma(g, a, batch, stream, ev[1]);
   if (e != hipSuccess) return fail(JACQ_KIVI_EHIP, "decode launch failed");
+  if (ev[2] && hipEventRecord(ev[2], stream) != hipSuccess)
+    return fail(JACQ_KIVI_EHIP, "hipEventRecord failed");
   return JACQ_KIVI_OK;
 }
 
@@ -348,6 +374,34 @@ int jacq_kivi_cache_append(const jacq_kivi_geometry* geo, uint8_t* K_CODE_PAGES,
 }
 
 // plan_batched_write, source_patch.py:504-553.
+int jacq_kivi_profile_start(int32_t max_calls) {
+  if (max_calls < 1) return fail(JACQ_KIVI_EINVAL, "max_calls must be >= 1");
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  while ((int)g_prof.ev.size() < 3 * max_calls) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return fail(JACQ_KIVI_EHIP, "hipEventCreate failed");
+    g_prof.ev.push_back(e);
+  }
+  g_prof.used = 0;
+  g_prof.on = true;
+  return JACQ_KIVI_OK;
+}
+
+int32_t jacq_kivi_profile_stop(float* kernel_ms, float* merge_ms, int32_t cap) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof.on = false;
+  const int n = g_prof.used < cap ? g_prof.used : cap;
+  for (int i = 0; i < n; ++i) {
+    hipEvent_t* e = &g_prof.ev[3 * i];
+    if (hipEventSynchronize(e[2]) != hipSuccess ||
+        hipEventElapsedTime(&kernel_ms[i], e[0], e[1]) != hipSuccess ||
+        hipEventElapsedTime(&merge_ms[i], e[1], e[2]) != hipSuccess)
+      return fail(JACQ_KIVI_EHIP, "event timing failed");
+  }
+  g_prof.used = 0;
+  return n;
+}
+
 int32_t jacq_kivi_plan_batched_write(int32_t start_seq_len, int32_t num_new, int32_t residual,
                                      int32_t group, jacq_kivi_subchunk* out, int32_t cap) {
   if (start_seq_len < 0)

@@ -229,11 +229,13 @@ __global__ __launch_bounds__(128) void kivi_combine_kernel(KiviGeo g, DecodeArgs
   a.out[(int64_t)b * a.out_stride + (int64_t)hq * g.hd + d] = acc * (1.0f / fmaxf(gl, 1.0e-30f));
 }
 
-hipError_t launch_decode(const KiviGeo& g, const DecodeArgs& a, int batch, hipStream_t stream) {
+hipError_t launch_decode(const KiviGeo& g, const DecodeArgs& a, int batch, hipStream_t stream,
+                         hipEvent_t between) {
   hipLaunchKernelGGL(kivi_decode_simple_kernel, dim3(a.max_splits, g.nkv, batch),
                      dim3(kDecThreads), 0, stream, g, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (between && (e = hipEventRecord(between, stream)) != hipSuccess) return e;
   if (a.max_splits > 1) {
     hipLaunchKernelGGL(kivi_combine_kernel, dim3(g.nh, batch), dim3(128), 0, stream, g, a);
     e = hipGetLastError();

@@ -836,7 +836,7 @@ static void launch_one(const KiviGeo& g, const DecodeArgs& a, hipStream_t stream
 }
 
 hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
-                              hipStream_t stream) {
+                              hipStream_t stream, hipEvent_t between) {
   if (g.hd == 128 && g.page == 16)
     launch_one<128, 16>(g, a, stream);
   else if (g.hd == 128)
@@ -847,6 +847,7 @@ hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
     launch_one<64, 32>(g, a, stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (between && (e = hipEventRecord(between, stream)) != hipSuccess) return e;
   hipLaunchKernelGGL(kivi_combine_stream_kernel, dim3(g.nkv, batch), dim3(256), 0, stream, g, a);
   return hipGetLastError();
 }

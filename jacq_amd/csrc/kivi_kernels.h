@@ -52,9 +52,12 @@ struct DecodeArgs {
 };
 
 hipError_t launch_append(const KiviGeo& g, const AppendArgs& a, int batch, hipStream_t stream);
-hipError_t launch_decode(const KiviGeo& g, const DecodeArgs& a, int batch, hipStream_t stream);
+// `between`, when not null, is recorded on the stream after the main kernel
+// and before the split-K merge (profiling).
+hipError_t launch_decode(const KiviGeo& g, const DecodeArgs& a, int batch, hipStream_t stream,
+                         hipEvent_t between = nullptr);
 hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
-                              hipStream_t stream);
+                              hipStream_t stream, hipEvent_t between = nullptr);
 // wavefronts the matrix-core decode launches on a device with `cus` CUs:
 // as many as are resident at once
 int decode_stream_waves(const KiviGeo& g, int cus);

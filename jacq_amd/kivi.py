@@ -127,12 +127,33 @@ def lib() -> ctypes.CDLL:
     L.jacq_kivi_plan_batched_write.argtypes = [_i32, _i32, _i32, _i32, ctypes.POINTER(Subchunk),
                                                _i32]
     L.jacq_kivi_plan_batched_write.restype = _i32
+    L.jacq_kivi_profile_start.argtypes = [_i32]
+    L.jacq_kivi_profile_start.restype = ctypes.c_int
+    L.jacq_kivi_profile_stop.argtypes = [ctypes.POINTER(ctypes.c_float),
+                                         ctypes.POINTER(ctypes.c_float), _i32]
+    L.jacq_kivi_profile_stop.restype = _i32
     _lib = L
     return L
 
 
 def last_error() -> str:
     return lib().jacq_kivi_last_error().decode()
+
+
+def profile_start(max_calls: int) -> None:
+    """Record HIP events around the next max_calls decode calls."""
+    if lib().jacq_kivi_profile_start(max_calls) != 0:
+        raise KiviLaunchError(last_error())
+
+
+def profile_stop(cap: int = 4096):
+    """(main-kernel ms, merge ms) per recorded decode call, in call order."""
+    k = (ctypes.c_float * cap)()
+    m = (ctypes.c_float * cap)()
+    n = lib().jacq_kivi_profile_stop(k, m, cap)
+    if n < 0:
+        raise KiviLaunchError(last_error())
+    return list(k[:n]), list(m[:n])
 
 
 def _ptr(t: torch.Tensor | None):

@@ -1,0 +1,218 @@
+"""Host side of the drop-in boundary, on the CPU: the C-ABI library loads and
+exports every function include/jacq_kivi.h declares, and its host-only
+entry points (validators, planner, versions) match the reference's tables.
+No GPU call is made here.
+
+Fixtures and tables:
+  * tests/golden/gpu_boundary_probe.json -- the reference's own width probe
+    (validation/vllm-2026-11-03/gpu-boundary-probe.json:1-62), also the cases
+    of tests/test_runtime_guards.py:164-201;
+  * byte math of tests/test_layout_and_scaffold.py:162-174;
+  * jac_launch argument order of tests/test_launch_signature.py:37-57;
+  * plan_batched_write (source_patch.py:504-553): no reference test pins its
+    outputs, so it is pinned by its invariants and against the oracle's C
+    restatement.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from jacq_amd import abi, bindings, kivi, layout
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "jacq_kivi.h")
+
+
+def header_functions() -> dict[str, list[str]]:
+    """name -> parameter identifiers of every function the header declares."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*([a-z_0-9]+)\s*\(([^)]*)\)\s*;",
+                         text, flags=re.M):
+        params = []
+        for p in m.group(2).split(","):
+            p = p.strip()
+            if p in ("", "void"):
+                continue
+            params.append(re.findall(r"[A-Za-z_][A-Za-z0-9_]*$", p)[0])
+        out[m.group(1)] = params
+    return out
+
+
+@pytest.fixture(scope="module")
+def native():
+    if not os.path.exists(kivi.library_path()):
+        pytest.fail(f"{kivi.library_path()} missing: run `python -m jacq_amd.build`")
+    return kivi.lib()
+
+
+def geo(**kw) -> kivi.Geometry:
+    base = dict(num_heads=40, num_kv_heads=8, head_dim=128, page_size=32, group_size=32,
+                residual=128, max_pages_per_seq=124, num_pages=1000)
+    base.update(kw)
+    return kivi.Geometry(*base.values())
+
+
+def test_header_declares_the_reference_symbols():
+    fns = header_functions()
+    for name in ("jac_launch", "jac_launch_tp2_local", "jac_launch_batched",
+                 "jac_launch_batched_tp2_local", "jac_launch_cache_write",
+                 "jac_launch_cache_write_batched", "kivi_cache_write_launch",
+                 "kivi_cache_write_batched_launch"):
+        assert name in fns, name
+    ext = sorted(n for n in fns if n.startswith("jacq_kivi_"))
+    assert ext == sorted([
+        "jacq_kivi_abi_version", "jacq_kivi_ext_version", "jacq_kivi_last_error",
+        "jacq_kivi_check_geometry", "jacq_kivi_max_seq_len", "jacq_kivi_check_block_table_width",
+        "jacq_kivi_decode_workspace_size", "jacq_kivi_decode", "jacq_kivi_cache_append",
+        "jacq_kivi_plan_batched_write", "jacq_kivi_profile_start", "jacq_kivi_profile_stop"])
+
+
+def test_library_exports_every_declared_function(native):
+    missing = [n for n in header_functions() if not hasattr(native, n)]
+    assert not missing, missing
+
+
+def test_jac_launch_argument_order_matches_reference():
+    params = header_functions()["jac_launch"]
+    assert params == ["Q", "BLOCK_TABLE", "K_CODE_PAGES", "K_SCALE_PAGES", "K_ZERO_PAGES",
+                      "V_CODE_PAGES", "V_SCALE_PAGES", "V_ZERO_PAGES", "K_RESIDUAL_SCRATCH",
+                      "V_RESIDUAL_SCRATCH", "SEQ_LEN", "O", "stream"]
+    order = list(bindings.JAC_LAUNCH_ORDER)
+    assert order[:-1] == params[:-1] and order[-1].endswith("stream")
+    assert "K_RESIDUAL" not in order and "V_RESIDUAL" not in order
+    batched = header_functions()["jac_launch_batched"]
+    assert batched[:3] == ["Q", "SEQ_LENS", "BLOCK_TABLE"] and batched[-3:] == [
+        "NUM_QUERIES", "O", "stream"]
+
+
+def test_versions(native):
+    assert native.jacq_kivi_abi_version() == abi.JACQ_KIVI_ABI_VERSION == 1
+    assert native.jacq_kivi_ext_version() == abi.JACQ_KIVI_EXT_VERSION
+
+
+def load_probe():
+    return json.load(open(os.path.join(ROOT, "tests", "golden", "gpu_boundary_probe.json")))
+
+
+def test_boundary_probe_python_validator():
+    for case in load_probe()["cases"]:
+        t = torch.zeros(case["width"], dtype=torch.int32)
+        if case["status"] == "accepted":
+            kivi.check_block_table_width(t, "BLOCK_TABLE", case["seq_len"])
+        else:
+            with pytest.raises(kivi.KiviCheckError, match="must be at least"):
+                kivi.check_block_table_width(t, "BLOCK_TABLE", case["seq_len"])
+    for bad in (0, 4097):  # test_runtime_guards.py:189-197
+        with pytest.raises(kivi.KiviCheckError):
+            kivi.check_block_table_width(torch.zeros(124, dtype=torch.int32), "BLOCK_TABLE", bad)
+
+
+def test_boundary_probe_native_validator(native):
+    probe = load_probe()
+    g = geo(**{k: v for k, v in probe["geometry"].items()})
+    for case in probe["cases"]:
+        rc = native.jacq_kivi_check_block_table_width(ctypes.byref(g), case["width"],
+                                                     case["seq_len"])
+        assert (rc == 0) == (case["status"] == "accepted"), case
+    for bad in (0, 4097):
+        assert native.jacq_kivi_check_block_table_width(ctypes.byref(g), 124, bad) != 0
+    assert native.jacq_kivi_max_seq_len(ctypes.byref(g)) == 4096
+
+
+def test_required_width_every_length(native):
+    """The width rule at page 16 and 32 for every length up to the cap:
+    floor((L - R) / 32) groups of 32 / P pages."""
+    for page in (16, 32):
+        g = geo(page_size=page, max_pages_per_seq=124 * 32 // page)
+        cap = native.jacq_kivi_max_seq_len(ctypes.byref(g))
+        assert cap == 4096
+        for L in range(1, cap + 1, 7):
+            need = max(0, (L - 128) // 32) * (32 // page)
+            assert native.jacq_kivi_check_block_table_width(ctypes.byref(g), need, L) == 0
+            if need:
+                assert native.jacq_kivi_check_block_table_width(ctypes.byref(g), need - 1, L) != 0
+
+
+@pytest.mark.parametrize("kw,ok", [
+    ({}, True),
+    (dict(page_size=16, max_pages_per_seq=248), True),
+    (dict(num_heads=20, num_kv_heads=4), True),
+    (dict(num_heads=32, num_kv_heads=4, head_dim=64), True),
+    (dict(num_heads=14, num_kv_heads=2, head_dim=64, residual=32), True),
+    (dict(head_dim=96), False),
+    (dict(page_size=8), False),
+    (dict(group_size=64), False),
+    (dict(residual=100), False),
+    (dict(num_heads=40, num_kv_heads=6), False),
+    (dict(num_heads=68, num_kv_heads=4), False),  # 17 query heads per kv head
+    (dict(num_pages=0), False),
+])
+def test_geometry_accept_reject(native, kw, ok):
+    assert (native.jacq_kivi_check_geometry(ctypes.byref(geo(**kw))) == 0) == ok
+    if not ok:
+        assert native.jacq_kivi_last_error()
+
+
+def test_layout_byte_math_matches_reference_fixture():
+    lay = layout.KiviPageLayout(layout.KiviModelGeometry.qwen25_coder_32b())
+    d = lay.to_abi_dict(seq_len=4096)
+    assert d["fp16_page_bytes_per_layer"] == 131_072
+    assert d["key_code_bytes"] == 16_384 and d["value_code_bytes"] == 16_384
+    assert d["key_scale_zero_bytes"] == 4_096 and d["value_scale_zero_bytes"] == 4_096
+    assert d["quantized_page_bytes_per_layer"] == 40_960
+    assert d["residual_pages"] == 4
+    assert d["effective_bytes_per_token_all_layers_at_seq_len"] == 87_552.0
+    assert 2.99 < d["capacity_ratio_vs_fp16_at_seq_len"] < 3.0
+    with pytest.raises(ValueError, match="block_size==group_size"):
+        layout.KiviPageLayout(layout.KiviModelGeometry.qwen25_coder_32b(),
+                              block_size=16).validate_for_vllm_lane()
+
+
+def test_decode_bytes_formula():
+    """160 bytes per token per kv head at HD=128, 80 at HD=64 (quantised part)."""
+    assert layout.decode_kv_bytes_per_token(128) == 160
+    assert layout.decode_kv_bytes_per_token(64) == 80
+
+
+def check_plan(plan, start, num, residual, group):
+    cap = residual + group
+    seq = start
+    for (s0, n, scratch_start, page, post) in plan:
+        assert s0 == seq and n >= 1
+        old = max(0, s0 - residual) // group * group
+        assert scratch_start == s0 - old
+        assert scratch_start + n <= cap, "a sub-chunk must fit the scratch"
+        new_old = max(0, s0 + n - residual) // group * group
+        assert new_old - old in (0, group), "at most one age-out per sub-chunk"
+        if new_old > old:
+            assert page == old // group and post == s0 + n - new_old
+        else:
+            assert page is None and post is None
+        seq += n
+    assert seq == start + num
+
+
+@pytest.mark.parametrize("residual,group", [(128, 32), (32, 32), (64, 32)])
+def test_plan_batched_write_invariants_and_oracle(native, oracle, residual, group):
+    rng = np.random.default_rng(residual)
+    cases = [(0, 1), (0, 160), (0, 161), (159, 2), (160, 1), (127, 300), (4000, 96)]
+    cases += [(int(a), int(b)) for a, b in zip(rng.integers(0, 5000, 60), rng.integers(1, 700, 60))]
+    for start, num in cases:
+        plan = kivi.plan_batched_write(start, num, residual, group)
+        check_plan(plan, start, num, residual, group)
+        assert plan == oracle.plan_batched_write(start, num, residual, group)
+
+
+def test_plan_batched_write_rejects_like_reference(native):
+    for start, num in ((-1, 4), (0, 0), (3, -2)):
+        with pytest.raises(ValueError):
+            kivi.plan_batched_write(start, num)
