@@ -127,7 +127,8 @@ void jac_launch_cache_write_batched(uint8_t* K_CODE_PAGES, jacq_half_t* K_SCALE_
 /* The hand-written writer's host entry, source_patch.py:624-629 / :1661-1697.
  * SLOT_MAPPING is accepted and ignored, as in the reference (:1667-1675).
  * NKV_RUNTIME selects 8 (global) or 4 (TP=2 local).  The reference declares
- * this with C++ linkage; here it has C linkage. */
+ * this with C++ linkage and __half pointers; that overload is exported too
+ * (end of this header), so a hipified reference binding links unchanged. */
 void kivi_cache_write_launch(uint8_t* K_CODE_PAGES, jacq_half_t* K_SCALE_PAGES,
                              jacq_half_t* K_ZERO_PAGES, uint8_t* V_CODE_PAGES,
                              jacq_half_t* V_SCALE_PAGES, jacq_half_t* V_ZERO_PAGES,
@@ -257,6 +258,31 @@ int32_t jacq_kivi_profile_stop(float* kernel_ms, float* merge_ms, int32_t cap);
 
 #ifdef __cplusplus
 }
+#endif
+
+#ifdef __cplusplus
+/* The two writer entry points with the reference's own C++ declaration
+ * (source_patch.py:624-637, `__half` and `cudaStream_t` as hipify maps
+ * them): same mangled names as the reference binding expects.  They forward
+ * to the C-linkage functions above. */
+#include <hip/hip_fp16.h>
+
+void kivi_cache_write_launch(unsigned char* K_CODE_PAGES, __half* K_SCALE_PAGES,
+                             __half* K_ZERO_PAGES, unsigned char* V_CODE_PAGES,
+                             __half* V_SCALE_PAGES, __half* V_ZERO_PAGES,
+                             __half* K_RESIDUAL_SCRATCH, __half* V_RESIDUAL_SCRATCH,
+                             const __half* NEW_K, const __half* NEW_V,
+                             const int64_t* SLOT_MAPPING, const int* BLOCK_TABLE, int seq_len,
+                             int NKV_RUNTIME, hipStream_t stream);
+
+void kivi_cache_write_batched_launch(unsigned char* K_CODE_PAGES, __half* K_SCALE_PAGES,
+                                     __half* K_ZERO_PAGES, unsigned char* V_CODE_PAGES,
+                                     __half* V_SCALE_PAGES, __half* V_ZERO_PAGES,
+                                     __half* K_RESIDUAL_SCRATCH, __half* V_RESIDUAL_SCRATCH,
+                                     const __half* NEW_K, const __half* NEW_V,
+                                     const int64_t* SLOT_MAPPING, const int* BLOCK_TABLE,
+                                     int START_SEQ_LEN, int NUM_NEW, int NKV_RUNTIME,
+                                     hipStream_t stream);
 #endif
 
 #endif /* JACQ_KIVI_H */

@@ -569,3 +569,39 @@ void kivi_cache_write_batched_launch(uint8_t* K_CODE_PAGES, jacq_half_t* K_SCALE
 }
 
 }  // extern "C"
+
+// C++-linkage writer entry points with the reference's parameter types
+// (source_patch.py:624-637): the mangled names a hipified reference binding
+// links against.  Thin forwards to the C-linkage functions.
+void kivi_cache_write_launch(unsigned char* K_CODE_PAGES, __half* K_SCALE_PAGES,
+                             __half* K_ZERO_PAGES, unsigned char* V_CODE_PAGES,
+                             __half* V_SCALE_PAGES, __half* V_ZERO_PAGES,
+                             __half* K_RESIDUAL_SCRATCH, __half* V_RESIDUAL_SCRATCH,
+                             const __half* NEW_K, const __half* NEW_V,
+                             const int64_t* SLOT_MAPPING, const int* BLOCK_TABLE, int seq_len,
+                             int NKV_RUNTIME, hipStream_t stream) {
+  auto h = [](const __half* p) { return reinterpret_cast<const jacq_half_t*>(p); };
+  auto m = [](__half* p) { return reinterpret_cast<jacq_half_t*>(p); };
+  kivi_cache_write_launch(K_CODE_PAGES, m(K_SCALE_PAGES), m(K_ZERO_PAGES), V_CODE_PAGES,
+                          m(V_SCALE_PAGES), m(V_ZERO_PAGES), m(K_RESIDUAL_SCRATCH),
+                          m(V_RESIDUAL_SCRATCH), h(NEW_K), h(NEW_V), SLOT_MAPPING,
+                          reinterpret_cast<const int32_t*>(BLOCK_TABLE), seq_len, NKV_RUNTIME,
+                          stream);
+}
+
+void kivi_cache_write_batched_launch(unsigned char* K_CODE_PAGES, __half* K_SCALE_PAGES,
+                                     __half* K_ZERO_PAGES, unsigned char* V_CODE_PAGES,
+                                     __half* V_SCALE_PAGES, __half* V_ZERO_PAGES,
+                                     __half* K_RESIDUAL_SCRATCH, __half* V_RESIDUAL_SCRATCH,
+                                     const __half* NEW_K, const __half* NEW_V,
+                                     const int64_t* SLOT_MAPPING, const int* BLOCK_TABLE,
+                                     int START_SEQ_LEN, int NUM_NEW, int NKV_RUNTIME,
+                                     hipStream_t stream) {
+  auto h = [](const __half* p) { return reinterpret_cast<const jacq_half_t*>(p); };
+  auto m = [](__half* p) { return reinterpret_cast<jacq_half_t*>(p); };
+  kivi_cache_write_batched_launch(K_CODE_PAGES, m(K_SCALE_PAGES), m(K_ZERO_PAGES), V_CODE_PAGES,
+                                  m(V_SCALE_PAGES), m(V_ZERO_PAGES), m(K_RESIDUAL_SCRATCH),
+                                  m(V_RESIDUAL_SCRATCH), h(NEW_K), h(NEW_V), SLOT_MAPPING,
+                                  reinterpret_cast<const int32_t*>(BLOCK_TABLE), START_SEQ_LEN,
+                                  NUM_NEW, NKV_RUNTIME, stream);
+}

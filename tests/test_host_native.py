@@ -216,3 +216,60 @@ def test_plan_batched_write_rejects_like_reference(native):
     for start, num in ((-1, 4), (0, 0), (3, -2)):
         with pytest.raises(ValueError):
             kivi.plan_batched_write(start, num)
+
+
+def _compile(tmp_path, name, src, cmd):
+    import subprocess
+    f = tmp_path / name
+    f.write_text(src)
+    r = subprocess.run(cmd[:1] + [str(f)] + cmd[1:], capture_output=True, text=True, cwd=tmp_path)
+    assert r.returncode == 0, r.stderr[-3000:]
+
+
+def test_header_compiles_as_c(tmp_path):
+    _compile(tmp_path, "c_user.c", '#include "jacq_kivi.h"\nint main(void){return jacq_kivi_abi_version() - 1;}\n',
+             ["gcc", "-std=c99", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__", f"-I{ROOT}/include",
+              "-I/opt/rocm/include"])
+
+
+def test_reference_style_cxx_binding_links(tmp_path):
+    """A translation unit declaring the writer entry points exactly as the
+    reference binding does (source_patch.py:570-658, hipified types) links
+    against the library: C symbols by name, the two C++ ones by mangled name."""
+    src = r'''
+#include <hip/hip_runtime_api.h>
+#include <hip/hip_fp16.h>
+#include <cstdint>
+extern "C" void jac_launch(const __half* Q, const int* BLOCK_TABLE,
+    const unsigned char* K_CODE_PAGES, const __half* K_SCALE_PAGES, const __half* K_ZERO_PAGES,
+    const unsigned char* V_CODE_PAGES, const __half* V_SCALE_PAGES, const __half* V_ZERO_PAGES,
+    const __half* K_RESIDUAL_SCRATCH, const __half* V_RESIDUAL_SCRATCH,
+    int SEQ_LEN, float* O, hipStream_t stream);
+void kivi_cache_write_launch(unsigned char* K_CODE_PAGES, __half* K_SCALE_PAGES,
+    __half* K_ZERO_PAGES, unsigned char* V_CODE_PAGES, __half* V_SCALE_PAGES,
+    __half* V_ZERO_PAGES, __half* K_RESIDUAL_SCRATCH, __half* V_RESIDUAL_SCRATCH,
+    const __half* NEW_K, const __half* NEW_V, const int64_t* SLOT_MAPPING,
+    const int* BLOCK_TABLE, int seq_len, int NKV_RUNTIME, hipStream_t stream);
+void kivi_cache_write_batched_launch(unsigned char* K_CODE_PAGES, __half* K_SCALE_PAGES,
+    __half* K_ZERO_PAGES, unsigned char* V_CODE_PAGES, __half* V_SCALE_PAGES,
+    __half* V_ZERO_PAGES, __half* K_RESIDUAL_SCRATCH, __half* V_RESIDUAL_SCRATCH,
+    const __half* NEW_K, const __half* NEW_V, const int64_t* SLOT_MAPPING,
+    const int* BLOCK_TABLE, int START_SEQ_LEN, int NUM_NEW, int NKV_RUNTIME, hipStream_t stream);
+int main(int argc, char**) {
+  if (argc > 99) {  // referenced, never called: no GPU work on the CPU
+    jac_launch(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+               nullptr, 0, nullptr, nullptr);
+    kivi_cache_write_launch(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                            nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, nullptr);
+    kivi_cache_write_batched_launch(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                    nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0,
+                                    0, nullptr);
+  }
+  return 0;
+}
+'''
+    lib_dir = os.path.dirname(kivi.library_path())
+    _compile(tmp_path, "binding.cpp", src,
+             ["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", "-o",
+              str(tmp_path / "binding"), f"-L{lib_dir}", "-ljacq_kivi", "-Wl,--no-as-needed",
+              f"-Wl,-rpath,{lib_dir}", "-L/opt/rocm/lib", "-lamdhip64"])
