@@ -389,34 +389,75 @@ __device__ inline half8_t softmax_tile(WaveState<HD>& st, floatx4 s0, floatx4 s1
   return pa;
 }
 
-// Dequantise the lane's V channels CPL*c + 2k (low nibbles) and + 2k + 1
-// (high nibbles) for its 8 tokens and accumulate PV.  x = 1024 + code (exact
-// fp16) gives code * s = fma(x, s, -1024 s) in one rounding.  When some
-// |scale| >= 64 (big, wave-uniform) -1024 s overflows fp16; then x - 1024 is
-// formed first (exact) and the addend is 0.  The adjustment is a branch
-// inside the same instruction stream, so both cases share registers.
+// V operands of one group kept in registers until its PV step: codes of rows
+// tok_v(j, e), and the scale / zero pairs of the lane's channel group for
+// tokens (tok_v(j, 2q), tok_v(j, 2q + 1)).
+struct VData {
+  uint32_t vc[8];
+  u32x4 vs4, vz4;
+};
+
+template <int HD, int P>
+__device__ inline VData load_v(const StageBuf<HD>* buf, const LaneMap& lm) {
+  using C = Cfg<HD, P>;
+  constexpr int HDG = C::HDG;
+  VData d;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint8_t* vp = &buf->v[lm.vread + 2 * e * C::HDP];
+    if constexpr (C::CPL == 8)
+      d.vc[e] = *(const uint32_t*)vp;
+    else
+      d.vc[e] = *(const uint16_t*)vp;
+  }
+  const uint8_t* vp = &buf->s[4 * HD + lm.vsread];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {  // pair q = e: tokens two rows apart
+    const uint8_t* p0 = vp + 8 * HDG * e;
+    d.vs4[e] = (uint32_t)*(const uint16_t*)p0 | ((uint32_t)*(const uint16_t*)(p0 + 4 * HDG) << 16);
+    d.vz4[e] = (uint32_t)*(const uint16_t*)(p0 + 64 * HDG) |
+               ((uint32_t)*(const uint16_t*)(p0 + 64 * HDG + 4 * HDG) << 16);
+  }
+  return d;
+}
+
+// |s| >= 64 somewhere in the wave's V scales (fp16 exponent field >= 0x15).
+// The OR of the bit patterns reaches the bound whenever one value does (and,
+// rarely, when none does, which only selects the slower exact arithmetic).
+__device__ inline bool big_scales(const VData& d) {
+  const uint32_t sor = (d.vs4[0] | d.vs4[1] | d.vs4[2] | d.vs4[3]) & 0x7FFF7FFFu;
+  const bool big = (sor & 0xFFFFu) >= 0x5400u || sor >= 0x54000000u;
+  return __builtin_amdgcn_ballot_w64(big) != 0;
+}
+
+// PV of one group, dequantising the lane's V channels CPL*c + 2k (low
+// nibbles) and + 2k + 1 (high nibbles) for its 8 tokens.  x = 1024 + code is
+// exact in fp16, so code * s = fma(x, s, -1024 s) with one rounding; the high
+// nibble carries 16x and uses s / 16.  When some |s| >= 64 (`big`,
+// wave-uniform) -1024 s and even code * s can leave the fp16 range: then x -
+// 1024 = code is formed first (exact), the products use s / 128 with a zero
+// addend and P carries the 128 back (powers of two: exact; P stays below
+// 2^15).  Both cases share one instruction stream and its registers.
 template <int HD>
-__device__ inline void pv_group(WaveState<HD>& st, half8_t pa, const uint32_t* vc, u32x4 vs4,
-                                const Nibble& nb, bool big) {
+__device__ inline void pv_group(WaveState<HD>& st, half8_t pa, const VData& d, const Nibble& nb,
+                                bool big) {
   constexpr int CPL = HD / 16;
-  const half8_t sv = as_h8(vs4);
-  const half8_t inv16 = {(_Float16)0.0625f, (_Float16)0.0625f, (_Float16)0.0625f,
-                         (_Float16)0.0625f, (_Float16)0.0625f, (_Float16)0.0625f,
-                         (_Float16)0.0625f, (_Float16)0.0625f};
-  const _Float16 off = big ? (_Float16)0.0f : (_Float16)-1024.f;
-  const half8_t offv = {off, off, off, off, off, off, off, off};
-  const u32x4 s_lo = vs4;
-  const half8_t shi = sv * inv16;
-  const u32x4 s_hi = as_u4(shi);
-  const u32x4 n_lo = as_u4(sv * offv);   // -1024 s (exact) or 0
-  const u32x4 n_hi = as_u4(shi * offv);  // -64 s (exact) or 0
+  const half8_t sv = as_h8(d.vs4);
+  const _Float16 f_lo = big ? (_Float16)(1.0f / 128.0f) : (_Float16)1.0f;
+  const _Float16 f_hi = big ? (_Float16)(1.0f / 2048.0f) : (_Float16)0.0625f;
+  const _Float16 f_n = big ? (_Float16)0.0f : (_Float16)-1024.0f;
+  const _Float16 f_p = big ? (_Float16)128.0f : (_Float16)1.0f;
+  const half8_t slo = sv * f_lo, shi = sv * f_hi;
+  const u32x4 s_lo = as_u4(slo), s_hi = as_u4(shi);
+  const u32x4 n_lo = as_u4(slo * f_n), n_hi = as_u4(shi * f_n);  // -1024 s (exact) or 0
+  const half8_t pv = pa * f_p;
   const half2_t m1024_2 = {(_Float16)-1024.f, (_Float16)-1024.f};
 #pragma unroll
   for (int k = 0; k < CPL / 2; ++k) {
     uint32_t xl[4], xh[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const uint32_t y = __builtin_amdgcn_perm(vc[2 * q + 1], vc[2 * q], nb.sel[k]);
+      const uint32_t y = __builtin_amdgcn_perm(d.vc[2 * q + 1], d.vc[2 * q], nb.sel[k]);
       xl[q] = (y & nb.lo) | nb.magic;  // (1024 + c, 1024 + c')
       xh[q] = (y & nb.hi) | nb.magic;  // (1024 + 16c, 1024 + 16c')
     }
@@ -433,8 +474,8 @@ __device__ inline void pv_group(WaveState<HD>& st, half8_t pa, const uint32_t* v
       lo[q] = as_u(__builtin_elementwise_fma(as_h2(xl[q]), as_h2(s_lo[q]), as_h2(n_lo[q])));
       hi[q] = as_u(__builtin_elementwise_fma(as_h2(xh[q]), as_h2(s_hi[q]), as_h2(n_hi[q])));
     }
-    st.o[2 * k] = mfma(pa, as_h8(lo), st.o[2 * k]);
-    st.o[2 * k + 1] = mfma(pa, as_h8(hi), st.o[2 * k + 1]);
+    st.o[2 * k] = mfma(pv, as_h8(lo), st.o[2 * k]);
+    st.o[2 * k + 1] = mfma(pv, as_h8(hi), st.o[2 * k + 1]);
   }
 }
 
@@ -445,31 +486,22 @@ struct SegCtx {
   half8_t qp[HD / 32];  // B operand of Q in the unpack order, odd channels / 16
 };
 
-// One quantised 32-token group (already in LDS): QK^T, online softmax, PV.
+// QK^T of one quantised group (already in LDS) and its online-softmax update:
+// S^T = K Q^T with B = q*s as fp16 hi + lo (lo = fma(q, s, -hi)); returns P
+// as the PV A operand.
 template <int HD, int P>
-__device__ inline void group_compute(WaveState<HD>& st, const SegCtx<HD>& q,
+__device__ inline half8_t qk_softmax(WaveState<HD>& st, const SegCtx<HD>& q,
                                      const StageBuf<HD>* buf, const LaneMap& lm, const Nibble& nb,
                                      float sscale, int lane) {
   using C = Cfg<HD, P>;
-  constexpr int KS = C::KS, CPL = C::CPL;
-  const int c = lane & 15, j = lane >> 4;
+  constexpr int KS = C::KS;
+  const int j = lane >> 4;
   const half8_t neg1024 = {(_Float16)-1024.f, (_Float16)-1024.f, (_Float16)-1024.f,
                            (_Float16)-1024.f, (_Float16)-1024.f, (_Float16)-1024.f,
                            (_Float16)-1024.f, (_Float16)-1024.f};
   typename C::kvec kc[2];
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) kc[tt] = *(const typename C::kvec*)&buf->k[lm.kread[tt]];
-  uint32_t vc[8];  // row tok_v(j, e)
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint8_t* vp = &buf->v[lm.vread + 2 * e * C::HDP];
-    if constexpr (CPL == 8)
-      vc[e] = *(const uint32_t*)vp;
-    else
-      vc[e] = *(const uint16_t*)vp;
-  }
-
-  // ---- S^T = K Q^T; B = q*s as fp16 hi + lo (lo = fma(q, s, -hi)) ----
   // three independent bias chains keep the dependent-MFMA latency short
   floatx4 bz = {0.f, 0.f, 0.f, 0.f}, bh = bz, bl = bz, s0 = bz, s1 = bz;
 #pragma unroll
@@ -492,27 +524,7 @@ __device__ inline void group_compute(WaveState<HD>& st, const SegCtx<HD>& q,
   }
   // every row of the bias tile holds the same per-head constant
   const float bias = bz[0] + (bh[0] + bl[0]);
-  const half8_t pa = softmax_tile<HD>(st, s0, s1, sscale, bias * sscale, j);
-
-  // ---- V dequant (packed fp16) and PV ----
-  // pair q: tokens tok_v(j, 2q) and tok_v(j, 2q + 1), two rows apart
-  constexpr int HDG = C::HDG;
-  const uint8_t* vp = &buf->s[4 * HD + lm.vsread];
-  u32x4 vs4, vz4;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint8_t* p0 = vp + 8 * HDG * e;
-    vs4[e] = (uint32_t)*(const uint16_t*)p0 | ((uint32_t)*(const uint16_t*)(p0 + 4 * HDG) << 16);
-    vz4[e] = (uint32_t)*(const uint16_t*)(p0 + 64 * HDG) |
-             ((uint32_t)*(const uint16_t*)(p0 + 64 * HDG + 4 * HDG) << 16);
-  }
-  st.ob = mfma(pa, as_h8(vz4), st.ob);
-  // |s| >= 64 is fp16 exponent field >= 0x15; the OR of the bit patterns
-  // reaches it whenever one value does (and, rarely, when none does, which
-  // only selects the exact-but-slower arithmetic)
-  const uint32_t sor = (vs4[0] | vs4[1] | vs4[2] | vs4[3]) & 0x7FFF7FFFu;
-  const bool big = (sor & 0xFFFFu) >= 0x5400u || sor >= 0x54000000u;
-  pv_group<HD>(st, pa, vc, vs4, nb, __builtin_amdgcn_ballot_w64(big) != 0);
+  return softmax_tile<HD>(st, s0, s1, sscale, bias * sscale, j);
 }
 
 // Tiles of one sequence: 32-token tiles of its decode window, at least one so
@@ -588,6 +600,45 @@ __device__ inline SeqSpan locate(const KiviGeo& g, const DecodeArgs& a, int64_t 
   return {a.batch, run, 1};
 }
 
+// One 32-token fp16 residual tile in registers: K rows of MFMA row c of tile
+// tt (tokens 8(c/4) + 4tt + c%4, channel block j) and V rows 8j..8j+7
+// (channels CPL*c..).  Rows past the end read row 0 of the tile (a valid
+// scratch row) and are masked by the caller.
+template <int HD>
+struct ResTile {
+  typedef typename std::conditional<HD == 128, u32x4, u32x2>::type vrow_t;
+  u32x4 kv[2][HD / 32];
+  vrow_t vr[8];
+};
+
+template <int HD>
+__device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, int b, int h,
+                                       int ov, int n, int tile, int lane) {
+  constexpr int KS = HD / 32, CPL = HD / 16;
+  const int c = lane & 15, j = lane >> 4;
+  const uint16_t* kscr = a.k_scr + (int64_t)b * a.scr_stride + (int64_t)h * g.rs * HD;
+  const uint16_t* vscr = a.v_scr + (int64_t)b * a.scr_stride + (int64_t)h * g.rs * HD;
+  const int t0 = tile * kGroup;
+  const int tn = min(kGroup, n - t0);
+  const int r0 = t0 - ov;  // scratch row of token t0
+  ResTile<HD> rt;
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int tl = 8 * (c >> 2) + 4 * tt + (c & 3);
+    const uint16_t* kr = kscr + (int64_t)(r0 + (tl < tn ? tl : 0)) * HD + j * (HD / 4);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      rt.kv[tt][ks] = __builtin_nontemporal_load((const u32x4*)(kr + 8 * ks));
+  }
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int tl = 8 * j + r;
+    rt.vr[r] = __builtin_nontemporal_load((const typename ResTile<HD>::vrow_t*)(
+        vscr + (int64_t)(r0 + (tl < tn ? tl : 0)) * HD + CPL * c));
+  }
+  return rt;
+}
+
 template <int HD, int P>
 __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, DecodeArgs a) {
   using C = Cfg<HD, P>;
@@ -620,7 +671,31 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
     const int t_beg = t;
     const int t_fin = (int)min((int64_t)T, t + (x1 - x));
 
-    // ---- segment setup: Q operands and softmax state ----
+    // ---- quantised groups: a ring of S LDS stages, S - 1 in flight ----
+    const int tq_end = min(t_fin, ov / kGroup);
+    // read-only for the whole launch: the constant address space lets the
+    // wave-uniform page reads be scalar loads (lgkmcnt, not vmcnt)
+    const __attribute__((address_space(4))) int32_t* bt =
+        (const __attribute__((address_space(4))) int32_t*)(a.block_tables +
+                                                           (int64_t)b * a.bt_stride);
+    const StageBases sb = stage_bases<HD, P>(a, NKV, h, lane);
+    auto page = [&](int tile, int k) -> uint32_t {
+      return (uint32_t)bt[tile * C::PPG + (C::PPG == 2 ? k : 0)];
+    };
+    uint32_t n0 = 0, n1 = 0;  // pages of group i + S - 1, read one group early
+    if (t_beg < tq_end) {
+      wait_vm<0>();  // the counts below see only this segment's DMAs
+#pragma unroll
+      for (int k = 0; k < S - 1; ++k)
+        if (t_beg + k < tq_end)
+          load_stage<HD, P>(&ring[k], sb, page(t_beg + k, 0), page(t_beg + k, 1), lane);
+      if (t_beg + S - 1 < tq_end) {
+        n0 = page(t_beg + S - 1, 0);
+        n1 = page(t_beg + S - 1, 1);
+      }
+    }
+
+    // ---- Q operands and softmax state (the loads overlap the first DMAs) ----
     SegCtx<HD> q;
     const uint16_t* qh = a.q + (int64_t)b * a.q_stride + (int64_t)h * G * HD;
 #pragma unroll
@@ -639,28 +714,8 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
     st.m = -1.0e30f;
     st.l = 0.0f;
 
-    // ---- quantised groups: a ring of S LDS stages, S - 1 in flight ----
-    const int tq_end = min(t_fin, ov / kGroup);
+    const int r_beg = max(t_beg, ov / kGroup);  // first fp16 residual tile
     if (t_beg < tq_end) {
-      // read-only for the whole launch: the constant address space lets the
-      // wave-uniform page reads be scalar loads (lgkmcnt, not vmcnt)
-      const __attribute__((address_space(4))) int32_t* bt =
-          (const __attribute__((address_space(4))) int32_t*)(a.block_tables +
-                                                             (int64_t)b * a.bt_stride);
-      const StageBases sb = stage_bases<HD, P>(a, NKV, h, lane);
-      auto page = [&](int tile, int k) -> uint32_t {
-        return (uint32_t)bt[tile * C::PPG + (C::PPG == 2 ? k : 0)];
-      };
-      wait_vm<0>();  // the counts below see only this loop's DMAs
-#pragma unroll
-      for (int k = 0; k < S - 1; ++k)
-        if (t_beg + k < tq_end)
-          load_stage<HD, P>(&ring[k], sb, page(t_beg + k, 0), page(t_beg + k, 1), lane);
-      uint32_t n0 = 0, n1 = 0;  // pages of group i + S - 1, read one group early
-      if (t_beg + S - 1 < tq_end) {
-        n0 = page(t_beg + S - 1, 0);
-        n1 = page(t_beg + S - 1, 1);
-      }
       int slot = 0;
       for (int i = t_beg; i < tq_end; ++i) {
         const int ahead = slot == 0 ? S - 1 : slot - 1;  // (slot + S - 1) % S
@@ -674,61 +729,43 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
         } else {
           wait_stages<L, S>(tq_end - 1 - i);
         }
-        group_compute<HD, P>(st, q, &ring[slot], lm, nb, sscale, lane);
+        const half8_t pa = qk_softmax<HD, P>(st, q, &ring[slot], lm, nb, sscale, lane);
+        const VData vd = load_v<HD, P>(&ring[slot], lm);
+        st.ob = mfma(pa, as_h8(vd.vz4), st.ob);  // sum_t P z_t
+        pv_group<HD>(st, pa, vd, nb, big_scales(vd));
         slot = slot == S - 1 ? 0 : slot + 1;
       }
     }
 
-    // ---- fp16 residual tiles ----
-    const uint16_t* kscr = a.k_scr + (int64_t)b * a.scr_stride + (int64_t)h * g.rs * HD;
-    const uint16_t* vscr = a.v_scr + (int64_t)b * a.scr_stride + (int64_t)h * g.rs * HD;
-    for (int i = max(t_beg, ov / kGroup); i < t_fin; ++i) {
-      const int t0 = i * kGroup;
-      const int tn = min(kGroup, n - t0);  // 0 only for an empty sequence
-      const int r0 = t0 - ov;              // scratch row of token t0
-      // every load is issued before the first use (rows past the end read
-      // row r0, a valid scratch row, and are masked afterwards)
-      u32x4 kv[2][KS];
+    // ---- fp16 residual tiles (all loads of a tile issued before its first use) ----
+    for (int i = r_beg; i < t_fin; ++i) {
+      ResTile<HD> cur = load_res<HD>(a, g, b, h, ov, n, i, lane);
+      const int tn = min(kGroup, n - i * kGroup);  // 0 only for an empty sequence
+      floatx4 sres[2];
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
-        const int tl = 8 * (c >> 2) + 4 * tt + (c & 3);
-        const uint16_t* kr = kscr + (int64_t)(r0 + (tl < tn ? tl : 0)) * HD + j * (HD / 4);
+        sres[tt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) kv[tt][ks] = __builtin_nontemporal_load((const u32x4*)(kr + 8 * ks));
-      }
-      typedef typename std::conditional<CPL == 8, u32x4, u32x2>::type vrow_t;
-      vrow_t vr[8];
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const int tl = 8 * j + r;
-        vr[r] = __builtin_nontemporal_load(
-            (const vrow_t*)(vscr + (int64_t)(r0 + (tl < tn ? tl : 0)) * HD + CPL * c));
-      }
-      floatx4 s[2];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        s[tt] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) s[tt] = mfma(as_h8(kv[tt][ks]), q.qn[ks], s[tt]);
+        for (int ks = 0; ks < KS; ++ks) sres[tt] = mfma(as_h8(cur.kv[tt][ks]), q.qn[ks], sres[tt]);
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii)
-          if (8 * j + 4 * tt + ii >= tn) s[tt][ii] = -INFINITY;
+          if (8 * j + 4 * tt + ii >= tn) sres[tt][ii] = -INFINITY;
       }
-      const half8_t pa = softmax_tile<HD>(st, s[0], s[1], sscale, 0.0f, j);
+      const half8_t pr = softmax_tile<HD>(st, sres[0], sres[1], sscale, 0.0f, j);
       // rows past the end carry P = 0 but must not carry NaN/Inf garbage
 #pragma unroll
       for (int r = 0; r < 8; ++r)
-        if (8 * j + r >= tn) vr[r] = vrow_t(0u);
+        if (8 * j + r >= tn) cur.vr[r] = typename ResTile<HD>::vrow_t(0u);
 #pragma unroll
       for (int nt = 0; nt < CPL; ++nt) {
         u32x4 vb;
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
-          const uint32_t va = vr[2 * qq][nt >> 1], vb2 = vr[2 * qq + 1][nt >> 1];  // rows 2qq, 2qq+1
+          const uint32_t va = cur.vr[2 * qq][nt >> 1], vb2 = cur.vr[2 * qq + 1][nt >> 1];
           vb[qq] = (nt & 1) ? __builtin_amdgcn_perm(vb2, va, 0x07060302u)
                             : __builtin_amdgcn_perm(vb2, va, 0x05040100u);
         }
-        st.o[nt] = mfma(pa, as_h8(vb), st.o[nt]);
+        st.o[nt] = mfma(pr, as_h8(vb), st.o[nt]);
       }
     }
 

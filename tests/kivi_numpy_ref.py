@@ -32,8 +32,11 @@ def decode_window(seq_len: int, residual: int, lq: int) -> tuple[int, int]:
     return old, res
 
 
-def dequant_sequence(cache, b: int, block_table: np.ndarray, seq_len: int):
-    """K, V [NKV, n, HD] float64 of the decode window of sequence b."""
+def dequant_sequence(cache, b: int, block_table: np.ndarray, seq_len: int,
+                     value_parts: bool = False):
+    """K, V [NKV, n, HD] float64 of the decode window of sequence b; with
+    value_parts, V is returned as (code * scale, zero) of the quantised tokens
+    (residual tokens: (value, 0))."""
     g = cache.geo
     page, hd, nkv = g.page, g.hd, g.nkv
     lq = (g.max_pages * page) // GROUP * GROUP
@@ -41,6 +44,7 @@ def dequant_sequence(cache, b: int, block_table: np.ndarray, seq_len: int):
     n = old + res
     K = np.zeros((nkv, n, hd))
     V = np.zeros((nkv, n, hd))
+    VZ = np.zeros((nkv, n, hd))
     kc = cache.k_code.reshape(-1)
     vc = cache.v_code.reshape(-1)
     ks = cache.k_scale.reshape(-1)
@@ -62,8 +66,11 @@ def dequant_sequence(cache, b: int, block_table: np.ndarray, seq_len: int):
             code = np.where(d % 2 == 0, byte & 0xF, byte >> 4).astype(np.float64)
             sidx = ((p * nkv + h) * page + slot) * (hd // GROUP) + d // GROUP
             V[h, t] = code * f16(vs[sidx]) + f16(vz[sidx])
+            VZ[h, t] = f16(vz[sidx])
         K[h, old:n] = f16(cache.k_scr[b, h, :res])
         V[h, old:n] = f16(cache.v_scr[b, h, :res])
+    if value_parts:
+        return K, (V - VZ, VZ)
     return K, V
 
 

@@ -278,3 +278,41 @@ def test_seq_len_zero_and_clamp(kivi):
     assert np.all(o_np[0] == 0)
     ref = o.decode_twopass(st.cache, 1, st.q[1], st.tables[1], cap + 1000)
     assert_close(o_np[1], ref, "clamped")
+
+
+def test_decode_extreme_value_scales(kivi):
+    """V tokens whose 32-channel ranges reach ~1e4: V scales >= 64 (where
+    -1024*s leaves fp16) and code*s products beyond 65504 take the scaled
+    path of the PV step.  Results stay finite and within the tolerance plus
+    the rounding of the fp16 MFMA operands (P, and code*s, each carry up to
+    2^-11 relative), 2^-10 * sum_t P_t (|code*s|_t + |zero|_t) -- with values
+    this large and outputs that cancel, that term exceeds 1e-2 * |O| (the
+    reference dequantises in fp32)."""
+    w = wl.WORKLOADS["qwen14b"]
+    st = State(w, lens=[700, 333], seed=5)
+    rng = np.random.default_rng(55)
+    for b in range(st.batch):
+        v = st.v_hist[b].view(np.float16).astype(np.float32)
+        pick = rng.random(v.shape[0]) < 0.3
+        v[pick] *= rng.choice([100.0, 3000.0, 9000.0], size=(int(pick.sum()), 1, 1))
+        st.v_hist[b] = np.clip(v, -65000, 65000).astype(np.float16).view(np.uint16)
+    st.build_oracle()
+    g = to_torch(st)
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, st.max_pages, st.num_pages)
+    cache = kivi.PagedKiviCache.from_tensors(geo, g)
+    q = torch.from_numpy(st.q).view(torch.float16).cuda()
+    out = cache.decode(q, torch.from_numpy(st.lens.astype(np.int32)).cuda(),
+                       torch.from_numpy(st.tables).cuda())
+    torch.cuda.synchronize()
+    ref = st.decode_ref()
+    got = out.cpu().numpy()
+    assert np.abs(ref).max() > 1000.0  # the case reaches the large-scale regime
+    assert np.isfinite(got).all()
+    from tests import kivi_numpy_ref as nref
+    for b in range(st.batch):
+        K, (cs, z) = nref.dequant_sequence(st.cache, b, st.tables[b], int(st.lens[b]),
+                                           value_parts=True)
+        mag = nref.attention(st.q[b], K, np.abs(cs) + np.abs(z))  # sum_t P_t (|cs| + |z|)
+        bound = 2e-3 + 1e-2 * np.abs(ref[b]) + 2.0 ** -10 * mag
+        err = np.abs(got[b] - ref[b])
+        assert (err <= bound).all(), f"seq {b}: worst excess {(err - bound).max():.3e}"
