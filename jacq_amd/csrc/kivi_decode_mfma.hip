@@ -489,7 +489,7 @@ struct SegCtx {
 // QK^T of one quantised group (already in LDS) and its online-softmax update:
 // S^T = K Q^T with B = q*s as fp16 hi + lo (lo = fma(q, s, -hi)); returns P
 // as the PV A operand.
-template <int HD, int P>
+template <int HD, int P, bool PACK>
 __device__ inline half8_t qk_softmax(WaveState<HD>& st, const SegCtx<HD>& q,
                                      const StageBuf<HD>* buf, const LaneMap& lm, const Nibble& nb,
                                      float sscale, int lane) {
@@ -502,8 +502,37 @@ __device__ inline half8_t qk_softmax(WaveState<HD>& st, const SegCtx<HD>& q,
   typename C::kvec kc[2];
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) kc[tt] = *(const typename C::kvec*)&buf->k[lm.kread[tt]];
-  // three independent bias chains keep the dependent-MFMA latency short
   floatx4 bz = {0.f, 0.f, 0.f, 0.f}, bh = bz, bl = bz, s0 = bz, s1 = bz;
+  if constexpr (PACK) {
+    // G <= 8: columns 0-7 carry q*s (hi) of heads 0-7, columns 8-15 the
+    // rounding remainder (lo) of the same heads, so one MFMA does both; a
+    // row_ror:8 add merges the halves (and leaves the sum in both lanes).
+    const bool hi_col = (lane & 15) < 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const uint8_t* kp = &buf->s[2 * (j * (HD / 4) + 8 * ks)];
+      const u32x4 sv = *(const u32x4*)kp;
+      const u32x4 zv = *(const u32x4*)(kp + 2 * HD);
+      const half8_t sp = as_h8(perm_pairs(sv));
+      const half8_t qs = q.qp[ks] * sp;
+      const half8_t ql = __builtin_elementwise_fma(q.qp[ks], sp, -qs);
+      const half8_t bq = hi_col ? qs : ql;
+      bz = mfma(as_h8(zv), q.qn[ks], bz);  // sum_d z_d q_gd
+      bh = mfma(neg1024, bq, bh);           // -1024 sum_d B_gd (hi | lo)
+      s0 = mfma(as_h8(unpack_codes(kc[0][ks], nb)), bq, s0);
+      s1 = mfma(as_h8(unpack_codes(kc[1][ks], nb)), bq, s1);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float t0 = s0[i] + bh[0], t1 = s1[i] + bh[0];
+      s0[i] = t0 + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                       0, __builtin_bit_cast(int, t0), 0x128, 0xF, 0xF, false));
+      s1[i] = t1 + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                       0, __builtin_bit_cast(int, t1), 0x128, 0xF, 0xF, false));
+    }
+    return softmax_tile<HD>(st, s0, s1, sscale, bz[0] * sscale, j);
+  }
+  // three independent bias chains keep the dependent-MFMA latency short
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     const uint8_t* kp = &buf->s[2 * (j * (HD / 4) + 8 * ks)];
@@ -639,7 +668,7 @@ __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, in
   return rt;
 }
 
-template <int HD, int P>
+template <int HD, int P, bool PACK>
 __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, DecodeArgs a) {
   using C = Cfg<HD, P>;
   constexpr int KS = C::KS, CPL = C::CPL;
@@ -701,7 +730,8 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (c < G) v = *(const u32x4*)(qh + c * HD + j * (HD / 4) + 8 * ks);
+      const int hq = PACK ? (c & 7) : c;  // packed: columns c and c + 8 share head c
+      if (hq < G) v = *(const u32x4*)(qh + hq * HD + j * (HD / 4) + 8 * ks);
       q.qn[ks] = as_h8(v);
       const half8_t div = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)0.0625f, (_Float16)0.0625f,
                            (_Float16)1.0f, (_Float16)1.0f, (_Float16)0.0625f, (_Float16)0.0625f};
@@ -729,7 +759,7 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
         } else {
           wait_stages<L, S>(tq_end - 1 - i);
         }
-        const half8_t pa = qk_softmax<HD, P>(st, q, &ring[slot], lm, nb, sscale, lane);
+        const half8_t pa = qk_softmax<HD, P, PACK>(st, q, &ring[slot], lm, nb, sscale, lane);
         const VData vd = load_v<HD, P>(&ring[slot], lm);
         st.ob = mfma(pa, as_h8(vd.vz4), st.ob);  // sum_t P z_t
         pv_group<HD>(st, pa, vd, nb, big_scales(vd));
@@ -869,7 +899,12 @@ __global__ __launch_bounds__(256) void kivi_combine_stream_kernel(KiviGeo g, Dec
 
 template <int HD, int P>
 static void launch_one(const KiviGeo& g, const DecodeArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((kivi_decode_stream_kernel<HD, P>), dim3(a.waves), dim3(64), 0, stream, g, a);
+  if (g.gqa <= 8)
+    hipLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, true>), dim3(a.waves), dim3(64), 0,
+                       stream, g, a);
+  else
+    hipLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, false>), dim3(a.waves), dim3(64), 0,
+                       stream, g, a);
 }
 
 hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
@@ -892,13 +927,13 @@ hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
 // One resident wavefront per slot: the tile stream is cut into as many runs as
 // the device holds waves of this kernel at once (registers and LDS decide how
 // many fit on a CU), so no CU idles and none runs a second round.
-template <int HD, int P>
+template <int HD, int P, bool PACK>
 static int resident_per_cu() {
   static int n = 0;
   if (n == 0) {
     int k = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, kivi_decode_stream_kernel<HD, P>, 64, 0) !=
-            hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, kivi_decode_stream_kernel<HD, P, PACK>,
+                                                     64, 0) != hipSuccess ||
         k < 1)
       k = 8;
     n = k;
@@ -906,16 +941,21 @@ static int resident_per_cu() {
   return n;
 }
 
+template <int HD, int P>
+static int resident_per_cu(const KiviGeo& g) {
+  return g.gqa <= 8 ? resident_per_cu<HD, P, true>() : resident_per_cu<HD, P, false>();
+}
+
 int decode_stream_waves(const KiviGeo& g, int cus) {
   int per = 8;
   if (g.hd == 128 && g.page == 16)
-    per = resident_per_cu<128, 16>();
+    per = resident_per_cu<128, 16>(g);
   else if (g.hd == 128)
-    per = resident_per_cu<128, 32>();
+    per = resident_per_cu<128, 32>(g);
   else if (g.page == 16)
-    per = resident_per_cu<64, 16>();
+    per = resident_per_cu<64, 16>(g);
   else
-    per = resident_per_cu<64, 32>();
+    per = resident_per_cu<64, 32>(g);
   return cus * per;
 }
 
