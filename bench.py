@@ -12,10 +12,12 @@ stream the kernels run on; a 512 MiB buffer is written before every step so
 the 256 MiB MALL and the L2 start cold.
 
 Prints ONE JSON line.  `value` is the effective KV bandwidth of the decode
-(algorithmic bytes / decode time, GB/s, both decode launches: the main kernel
-and the split-K merge); `ms_per_step` is that decode time per step.
-`roofline.achieved` is the same bytes over the main kernel alone, timed with
-HIP events the library records on the launch stream (jacq_kivi_profile_*).  The CPU baseline runs the oracle (oracle/, a C restatement of the
+(algorithmic bytes / decode time, GB/s); the decode time is the GPU time of
+both decode launches (main kernel + split-K merge) from HIP events the library
+records on the launch stream (jacq_kivi_profile_*), and `ms_per_step` is that
+time per step.  `roofline.achieved` is the same bytes over the main kernel
+alone.  `host_bracketed_us` adds the host-side gaps (Python argument checks
+before each launch) seen by events recorded around the Python calls.  The CPU baseline runs the oracle (oracle/, a C restatement of the
 reference path) over the same state on this host's cores.
 """
 from __future__ import annotations
@@ -143,18 +145,25 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     kern_ms, merge_ms = kivi.profile_stop(total_steps)
+    write_ms = kivi.profile_write_ms(total_steps)
     kern = np.array(kern_ms[args.warmup:])
     merge = np.array(merge_ms[args.warmup:])
+    wgpu = np.array(write_ms[args.warmup:])
 
-    dec_ms, wr_ms, step_bytes = [], [], []
+    host_dec_ms, host_wr_ms, step_bytes = [], [], []
     for i in range(args.warmup, total_steps):
         e = evs[i]
-        wr_ms.append(e[0].elapsed_time(e[1]))
-        dec_ms.append(e[1].elapsed_time(e[2]))
+        host_wr_ms.append(e[0].elapsed_time(e[1]))
+        host_dec_ms.append(e[1].elapsed_time(e[2]))
         step_bytes.append(layout.decode_step_bytes(lens0 + i + 1, w.nh, w.nkv, w.hd, w.page,
                                                    w.residual, w.group))
-    dec = np.array(dec_ms)
-    wr = np.array(wr_ms)
+    # GPU time of the decode: main kernel + split-K merge, from the events the
+    # library records on the launch stream (host-side gaps before a launch,
+    # e.g. Python argument checks, are excluded; host_bracketed_* keep them)
+    dec = kern + merge
+    wr = wgpu
+    host_dec = np.array(host_dec_ms)
+    host_wr = np.array(host_wr_ms)
     gbs = float(np.sum(step_bytes) / (dec.sum() * 1e-3) / 1e9)
     kern_gbs = float(np.sum(step_bytes) / (kern.sum() * 1e-3) / 1e9)
     bytes_per_step = float(np.mean(step_bytes))
@@ -198,6 +207,8 @@ def main() -> int:
         "merge_us": {"mean": round(float(merge.mean()) * 1e3, 2)},
         "write_us": {"mean": round(float(wr.mean()) * 1e3, 2),
                      "median": round(float(np.median(wr)) * 1e3, 2)},
+        "host_bracketed_us": {"decode": round(float(host_dec.mean()) * 1e3, 2),
+                              "write": round(float(host_wr.mean()) * 1e3, 2)},
         "step_us_write_plus_decode": round(float((dec + wr).mean()) * 1e3, 2),
         "decode_bytes_per_step": int(bytes_per_step),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),

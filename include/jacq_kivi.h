@@ -248,13 +248,16 @@ int32_t jacq_kivi_plan_batched_write(int32_t start_seq_len, int32_t num_new, int
 
 /* Measurement hook (no counterpart in the reference; for benchmarks and
  * profilers).  jacq_kivi_profile_start enables recording for the next
- * max_calls decode calls: each records HIP events on its own stream around
- * its main kernel and its split-K merge.  jacq_kivi_profile_stop disables
- * recording, waits for the events and writes the per-call milliseconds of
- * the main kernel and of the merge (at most cap entries); it returns the
- * number of calls written or -1. */
+ * max_calls decode calls and max_calls cache-write calls: each records HIP
+ * events on its own stream around its kernels.  jacq_kivi_profile_stop
+ * disables recording, waits for the events and writes the per-call
+ * milliseconds of the decode main kernel and of its split-K merge (at most
+ * cap entries); it returns the number of decode calls written or -1.
+ * jacq_kivi_profile_write_ms then writes the per-call milliseconds of the
+ * cache-write kernel recorded in the same window. */
 int jacq_kivi_profile_start(int32_t max_calls);
 int32_t jacq_kivi_profile_stop(float* kernel_ms, float* merge_ms, int32_t cap);
+int32_t jacq_kivi_profile_write_ms(float* ms, int32_t cap);
 
 #ifdef __cplusplus
 }

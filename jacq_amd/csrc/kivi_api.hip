@@ -177,8 +177,9 @@ void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& 
 // kernel, between it and the split-K merge, and after the merge.
 struct Profiler {
   bool on = false;
-  int used = 0;
-  std::vector<hipEvent_t> ev;  // 3 per call
+  int used = 0, wused = 0;
+  std::vector<hipEvent_t> ev;   // decode: 3 per call
+  std::vector<hipEvent_t> wev;  // cache write: 2 per call
 };
 std::mutex g_prof_mu;
 Profiler g_prof;
@@ -188,6 +189,13 @@ void profile_slot(hipEvent_t out[3]) {
   if (!g_prof.on || 3 * (g_prof.used + 1) > (int)g_prof.ev.size()) return;
   for (int i = 0; i < 3; ++i) out[i] = g_prof.ev[3 * g_prof.used + i];
   ++g_prof.used;
+}
+
+void profile_write_slot(hipEvent_t out[2]) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  if (!g_prof.on || 2 * (g_prof.wused + 1) > (int)g_prof.wev.size()) return;
+  for (int i = 0; i < 2; ++i) out[i] = g_prof.wev[2 * g_prof.wused + i];
+  ++g_prof.wused;
 }
 
 // Decode with a runtime geometry; seq_len_host >= 0 when the (single) length
@@ -276,8 +284,14 @@ int run_append(const jacq_kivi_geometry& x, uint8_t* kc, jacq_half_t* ksc, jacq_
   a.start_lens = start_lens;
   a.start_len = start_len;
   a.num_new = num_new;
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  profile_write_slot(ev);
+  if (ev[0] && hipEventRecord(ev[0], stream) != hipSuccess)
+    return fail(JACQ_KIVI_EHIP, "hipEventRecord failed");
   if (jacq::launch_append(g, a, batch, stream) != hipSuccess)
     return fail(JACQ_KIVI_EHIP, "cache-write launch failed");
+  if (ev[1] && hipEventRecord(ev[1], stream) != hipSuccess)
+    return fail(JACQ_KIVI_EHIP, "hipEventRecord failed");
   return JACQ_KIVI_OK;
 }
 
@@ -377,12 +391,16 @@ int jacq_kivi_cache_append(const jacq_kivi_geometry* geo, uint8_t* K_CODE_PAGES,
 int jacq_kivi_profile_start(int32_t max_calls) {
   if (max_calls < 1) return fail(JACQ_KIVI_EINVAL, "max_calls must be >= 1");
   std::lock_guard<std::mutex> lk(g_prof_mu);
-  while ((int)g_prof.ev.size() < 3 * max_calls) {
-    hipEvent_t e = nullptr;
-    if (hipEventCreate(&e) != hipSuccess) return fail(JACQ_KIVI_EHIP, "hipEventCreate failed");
-    g_prof.ev.push_back(e);
+  for (auto* pool : {&g_prof.ev, &g_prof.wev}) {
+    const size_t want = (pool == &g_prof.ev ? 3u : 2u) * (size_t)max_calls;
+    while (pool->size() < want) {
+      hipEvent_t e = nullptr;
+      if (hipEventCreate(&e) != hipSuccess) return fail(JACQ_KIVI_EHIP, "hipEventCreate failed");
+      pool->push_back(e);
+    }
   }
   g_prof.used = 0;
+  g_prof.wused = 0;
   g_prof.on = true;
   return JACQ_KIVI_OK;
 }
@@ -399,6 +417,19 @@ int32_t jacq_kivi_profile_stop(float* kernel_ms, float* merge_ms, int32_t cap) {
       return fail(JACQ_KIVI_EHIP, "event timing failed");
   }
   g_prof.used = 0;
+  return n;
+}
+
+int32_t jacq_kivi_profile_write_ms(float* ms, int32_t cap) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  const int n = g_prof.wused < cap ? g_prof.wused : cap;
+  for (int i = 0; i < n; ++i) {
+    hipEvent_t* e = &g_prof.wev[2 * i];
+    if (hipEventSynchronize(e[1]) != hipSuccess ||
+        hipEventElapsedTime(&ms[i], e[0], e[1]) != hipSuccess)
+      return fail(JACQ_KIVI_EHIP, "event timing failed");
+  }
+  g_prof.wused = 0;
   return n;
 }
 

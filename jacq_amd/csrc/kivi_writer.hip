@@ -18,6 +18,11 @@ namespace jacq {
 
 constexpr int kWriterThreads = 256;
 
+// 16-byte vector as a native vector type: arrays of it stay in registers
+// (HIP's uint4 class does not).
+typedef uint32_t w4 __attribute__((ext_vector_type(4)));
+typedef uint32_t w2 __attribute__((ext_vector_type(2)));
+
 #pragma clang fp contract(off)
 
 __device__ inline int clamp_code(float x) {  // source_patch.py:1517-1522
@@ -27,13 +32,22 @@ __device__ inline int clamp_code(float x) {  // source_patch.py:1517-1522
   return code;
 }
 
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
+// operations, not for its global stores (those have no reader in the kernel).
+// The memory clobber keeps the compiler from moving LDS accesses across it.
+__device__ inline void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Compare-and-select running min/max: ties (+0 / -0) keep the earlier value.
 __device__ inline float min_keep(float cur, float x) { return x < cur ? x : cur; }
 __device__ inline float max_keep(float cur, float x) { return x > cur ? x : cur; }
 
-__global__ __launch_bounds__(kWriterThreads) void kivi_append_kernel(KiviGeo g, AppendArgs a) {
-  __shared__ uint4 k_tile[kGroup * 128 / 8];  // 32 tokens x HD fp16, HD <= 128
-  __shared__ uint4 v_tile[kGroup * 128 / 8];
+__global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(2))) void kivi_append_kernel(KiviGeo g, AppendArgs a) {
+  __shared__ w4 k_tile[kGroup * 128 / 8];  // 32 tokens x HD fp16, HD <= 128
+  __shared__ w4 v_tile[kGroup * 128 / 8];
+  __shared__ w4 k_code_tile[kGroup * 64 / 16];  // 32 tokens x HD/2 code bytes
+  __shared__ w4 v_code_tile[kGroup * 64 / 16];
 
   const int h = blockIdx.x;
   const int b = blockIdx.y;
@@ -63,132 +77,215 @@ __global__ __launch_bounds__(kWriterThreads) void kivi_append_kernel(KiviGeo g, 
   const uint16_t* nv = a.new_v + (int64_t)b * a.new_stride + (int64_t)h * HD;
   const int32_t* bt = a.block_tables + (int64_t)b * a.bt_stride;
 
-  // Phase 1 (reference order): append rows [r0, r0+n) of the scratch
-  // (append_scratch_token_kernel / append_scratch_tokens_batched_kernel).
-  if (in_scratch) {
-    for (int i = tid; i < n * VPR; i += kWriterThreads) {
-      const int r = i / VPR, c = i % VPR;
-      *(uint4*)(ks + (int64_t)(r0 + r) * HD + c * 8) = *(const uint4*)(nk + r * tok_stride + c * 8);
-      *(uint4*)(vs + (int64_t)(r0 + r) * HD + c * 8) = *(const uint4*)(nv + r * tok_stride + c * 8);
-    }
-    __syncthreads();
-  }
-
   // Row p of the concatenated stream [scratch rows 0..r0) ++ [new tokens].
+  // Appended rows are always read from NEW_K / NEW_V, so nothing below reads
+  // what this kernel writes to the scratch.
   auto krow = [&](int p) -> const uint16_t* {
-    if (in_scratch || p < r0) return ks + (int64_t)p * HD;
+    if (p < r0) return ks + (int64_t)p * HD;
     return nk + (int64_t)(p - r0) * tok_stride;
   };
   auto vrow = [&](int p) -> const uint16_t* {
-    if (in_scratch || p < r0) return vs + (int64_t)p * HD;
+    if (p < r0) return vs + (int64_t)p * HD;
     return nv + (int64_t)(p - r0) * tok_stride;
   };
 
+  // Shift sources of the first pass (phase 3), loaded now so that their
+  // latency overlaps the quantisation.
+  constexpr int kShiftRows = 128;
+  constexpr int kPer = kShiftRows * 16 / kWriterThreads;  // w4 per thread per array, HD <= 128
+  const bool shift = !(in_scratch && D == 0);
+  w4 shk[kPer], shv[kPer];
+  const int rows0 = shift ? min(kShiftRows, r1) : 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = tid + j * kWriterThreads;
+    if (i < rows0 * VPR) {
+      const int r = i / VPR, c = i % VPR;
+      shk[j] = *(const w4*)(krow(D + r) + c * 8);
+      shv[j] = *(const w4*)(vrow(D + r) + c * 8);
+    }
+  }
+
+  // The first aged group's 32 rows go to LDS (the stores below cannot touch
+  // them: phase 1 writes rows >= r0, the shift only after its barrier).
+  auto load_tile = [&](int gi) {
+    for (int i = tid; i < kGroup * VPR; i += kWriterThreads) {
+      const int t = i / VPR, c = i % VPR;
+      k_tile[i] = *(const w4*)(krow(gi * kGroup + t) + c * 8);
+      v_tile[i] = *(const w4*)(vrow(gi * kGroup + t) + c * 8);
+    }
+  };
+  if (D > 0) load_tile(0);
+
+  // Every load above lands before any store below (wait + barrier).
+  __syncthreads();
+
+  // Phase 1 (reference order: append, then age out, then shift): in the
+  // in-scratch case the appended rows [r0, r0+n) that the shift does not
+  // overwrite, i.e. [max(r0, r1'), r0+n) with r1' = r1 when a group ages out,
+  // stay visible (as live rows or as the reference's stale rows).  The shift
+  // rewrites the others, so they are not stored and no store of this kernel
+  // is ordered against another (append_scratch_token_kernel /
+  // append_scratch_tokens_batched_kernel).
+  if (in_scratch) {
+    const int keep_from = D > 0 ? max(r0, r1) : r0;
+    for (int i = tid; i < (r0 + n - keep_from) * VPR; i += kWriterThreads) {
+      const int r = keep_from + i / VPR, c = i % VPR;
+      *(w4*)(ks + (int64_t)r * HD + c * 8) = *(const w4*)(krow(r) + c * 8);
+      *(w4*)(vs + (int64_t)r * HD + c * 8) = *(const w4*)(vrow(r) + c * 8);
+    }
+  }
+
   // Phase 2: quantise each aged group (pack_key/pack_value_age_out_page_kernel).
+  // Every thread works: K uses four threads per channel pair (8 tokens each),
+  // V two threads per (token, 32-channel group) (16 channels each); the
+  // partial min / max are merged in index order with the same compare-select
+  // as one running loop, so ties resolve to the same (earliest) value.  Codes
+  // are packed into LDS and stored as whole 16-byte row pieces.
+  uint8_t* const kcode_tile = (uint8_t*)k_code_tile;
+  uint8_t* const vcode_tile = (uint8_t*)v_code_tile;
   for (int gi = 0; gi < D / kGroup; ++gi) {
     const int lg = old0 / kGroup + gi;
     const int first_page = lg * ppg;
-    for (int i = tid; i < kGroup * VPR; i += kWriterThreads) {
-      const int t = i / VPR, c = i % VPR;
-      k_tile[i] = *(const uint4*)(krow(gi * kGroup + t) + c * 8);
-      v_tile[i] = *(const uint4*)(vrow(gi * kGroup + t) + c * 8);
+    if (gi > 0) {
+      load_tile(gi);
+      lds_barrier();
     }
-    __syncthreads();
     const bool table_ok = first_page + ppg <= g.max_pages;
     const uint16_t* kt = (const uint16_t*)k_tile;
     const uint16_t* vt = (const uint16_t*)v_tile;
-    if (table_ok && tid < HDP) {
-      // K: channels d0 = 2*tid, d1 = d0 + 1 over the group's 32 tokens.
-      const int d0 = 2 * tid;
-      float mn0 = h2f(kt[d0]), mx0 = mn0, mn1 = h2f(kt[d0 + 1]), mx1 = mn1;
-      for (int t = 1; t < kGroup; ++t) {
+    if (tid < 2 * HD) {
+      // K: channel pair p = tid / 4 (channels 2p, 2p + 1), tokens 8q..8q+7.
+      const int pr = tid >> 2, q = tid & 3, d0 = 2 * pr, t0 = 8 * q;
+      float mn0 = h2f(kt[t0 * HD + d0]), mx0 = mn0;
+      float mn1 = h2f(kt[t0 * HD + d0 + 1]), mx1 = mn1;
+#pragma unroll
+      for (int t = t0 + 1; t < t0 + 8; ++t) {
         const float x0 = h2f(kt[t * HD + d0]), x1 = h2f(kt[t * HD + d0 + 1]);
         mn0 = min_keep(mn0, x0);
         mx0 = max_keep(mx0, x0);
         mn1 = min_keep(mn1, x1);
         mx1 = max_keep(mx1, x1);
       }
+#pragma unroll
+      for (int off = 1; off < 4; off <<= 1) {  // merge quarters in token order
+        const bool first = (q & off) == 0;    // this lane holds the earlier tokens
+        const float on0 = __shfl_xor(mn0, off, 64), ox0 = __shfl_xor(mx0, off, 64);
+        const float on1 = __shfl_xor(mn1, off, 64), ox1 = __shfl_xor(mx1, off, 64);
+        mn0 = first ? min_keep(mn0, on0) : min_keep(on0, mn0);
+        mx0 = first ? max_keep(mx0, ox0) : max_keep(ox0, mx0);
+        mn1 = first ? min_keep(mn1, on1) : min_keep(on1, mn1);
+        mx1 = first ? max_keep(mx1, ox1) : max_keep(ox1, mx1);
+      }
       float s0 = (mx0 - mn0) / 15.0f;
       float s1 = (mx1 - mn1) / 15.0f;
       if (!(s0 > 0.0f)) s0 = 1.0f;
       if (!(s1 > 0.0f)) s1 = 1.0f;
-      const uint32_t sc = (uint32_t)f2h(s0) | ((uint32_t)f2h(s1) << 16);
-      const uint32_t zr = (uint32_t)f2h(mn0) | ((uint32_t)f2h(mn1) << 16);
-      for (int pg = 0; pg < ppg; ++pg) {
-        const int phys = bt[first_page + pg];
-        if (phys < 0 || phys >= g.num_pages) continue;
-        const int64_t base = ((int64_t)phys * g.nkv + h) * HD + d0;
-        *(uint32_t*)(a.k_scale + base) = sc;
-        *(uint32_t*)(a.k_zero + base) = zr;
+      if (q == 0 && table_ok) {
+        const uint32_t sc = (uint32_t)f2h(s0) | ((uint32_t)f2h(s1) << 16);
+        const uint32_t zr = (uint32_t)f2h(mn0) | ((uint32_t)f2h(mn1) << 16);
+        for (int pg = 0; pg < ppg; ++pg) {
+          const int phys = bt[first_page + pg];
+          if (phys < 0 || phys >= g.num_pages) continue;
+          const int64_t base = ((int64_t)phys * g.nkv + h) * HD + d0;
+          *(uint32_t*)(a.k_scale + base) = sc;
+          *(uint32_t*)(a.k_zero + base) = zr;
+        }
       }
-      for (int t = 0; t < kGroup; ++t) {
-        const int phys = bt[first_page + t / P];
-        if (phys < 0 || phys >= g.num_pages) continue;
+#pragma unroll
+      for (int t = t0; t < t0 + 8; ++t) {
         const int c0 = clamp_code((h2f(kt[t * HD + d0]) - mn0) / s0);
         const int c1 = clamp_code((h2f(kt[t * HD + d0 + 1]) - mn1) / s1);
-        a.k_code[(((int64_t)phys * g.nkv + h) * P + (t % P)) * HDP + tid] =
-            (uint8_t)((c0 & 0x0f) | ((c1 & 0x0f) << 4));
+        kcode_tile[t * HDP + pr] = (uint8_t)((c0 & 0x0f) | ((c1 & 0x0f) << 4));
       }
-    } else if (table_ok && tid >= HDP && tid < HDP + kGroup * HDG) {
-      // V: token t, channel group cg, over 32 channels.
-      const int j = tid - HDP;
-      const int t = j / HDG, cg = j % HDG;
-      const uint16_t* row = vt + t * HD + cg * kGroup;
+    }
+    if (tid < 2 * kGroup * HDG) {
+      // V: (token t, channel group cg) = tid / 2, channels 16 * (tid % 2) .. + 15.
+      const int pr = tid >> 1, hf = tid & 1;
+      const int t = pr / HDG, cg = pr % HDG;
+      const uint16_t* row = vt + t * HD + cg * kGroup + 16 * hf;
       float mn = h2f(row[0]), mx = mn;
-      for (int c = 1; c < kGroup; ++c) {
+#pragma unroll
+      for (int c = 1; c < 16; ++c) {
         const float x = h2f(row[c]);
         mn = min_keep(mn, x);
         mx = max_keep(mx, x);
       }
-      float s = (mx - mn) / 15.0f;
-      if (!(s > 0.0f)) s = 1.0f;
-      uint32_t packed[4];
-      for (int w = 0; w < 4; ++w) {
+      const float on = __shfl_xor(mn, 1, 64), ox = __shfl_xor(mx, 1, 64);
+      mn = hf == 0 ? min_keep(mn, on) : min_keep(on, mn);
+      mx = hf == 0 ? max_keep(mx, ox) : max_keep(ox, mx);
+      float sv = (mx - mn) / 15.0f;
+      if (!(sv > 0.0f)) sv = 1.0f;
+      uint32_t packed[2];
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
         uint32_t word = 0;
+#pragma unroll
         for (int k = 0; k < 8; ++k) {
-          const int code = clamp_code((h2f(row[w * 8 + k]) - mn) / s);
+          const int code = clamp_code((h2f(row[w * 8 + k]) - mn) / sv);
           word |= (uint32_t)code << (4 * k);
         }
         packed[w] = word;
       }
-      const int phys = bt[first_page + t / P];
-      if (phys >= 0 && phys < g.num_pages) {
-        const int64_t tok = ((int64_t)phys * g.nkv + h) * P + (t % P);
-        *(uint4*)(a.v_code + tok * HDP + cg * (kGroup / 2)) =
-            make_uint4(packed[0], packed[1], packed[2], packed[3]);
-        a.v_scale[tok * HDG + cg] = f2h(s);
-        a.v_zero[tok * HDG + cg] = f2h(mn);
+      *(w2*)(vcode_tile + t * HDP + cg * (kGroup / 2) + 8 * hf) = w2{packed[0], packed[1]};
+      if (hf == 0 && table_ok) {
+        const int phys = bt[first_page + t / P];
+        if (phys >= 0 && phys < g.num_pages) {
+          const int64_t tok = ((int64_t)phys * g.nkv + h) * P + (t % P);
+          a.v_scale[tok * HDG + cg] = f2h(sv);
+          a.v_zero[tok * HDG + cg] = f2h(mn);
+        }
       }
     }
-    __syncthreads();
+    lds_barrier();
+    // packed codes: 32 rows of HD/2 bytes each for K and V, 16 bytes per thread
+    if (table_ok) {
+      const int RPC = HDP / 16;  // 16-byte pieces per code row
+      for (int i = tid; i < 2 * kGroup * RPC; i += kWriterThreads) {
+        const int kv = i / (kGroup * RPC), r = (i / RPC) % kGroup, c = i % RPC;
+        const int phys = bt[first_page + r / P];
+        if (phys < 0 || phys >= g.num_pages) continue;
+        uint8_t* dst = (kv ? a.v_code : a.k_code) +
+                       (((int64_t)phys * g.nkv + h) * P + (r % P)) * HDP + 16 * c;
+        *(w4*)dst = *(const w4*)((kv ? vcode_tile : kcode_tile) + r * HDP + 16 * c);
+      }
+    }
+    lds_barrier();  // the tiles are rewritten by the next group
   }
 
   // Phase 3: scratch rows [0, r1) <- stream rows [D, D + r1)
   // (shift_scratch_after_age_out_kernel; nothing to do without an age-out in
-  // the in-scratch case, where phase 1 already placed the new rows).
-  if (in_scratch && D == 0) return;
-  for (int blk = 0; blk * kGroup < r1; ++blk) {
-    const int rows = min(kGroup, r1 - blk * kGroup);
-    uint4 kv[2], vv[2];
+  // the in-scratch case, where phase 1 already placed the new rows).  Up to
+  // 128 rows per pass: every load of a pass (and every scratch read of phase
+  // 2) lands before any of its stores (wait + barrier), and a later pass's
+  // stores follow every earlier load.
+  if (!shift) return;
+  for (int r_base = 0; r_base < r1; r_base += kShiftRows) {
+    const int rows = min(kShiftRows, r1 - r_base);
+    if (r_base > 0) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int i = tid + j * kWriterThreads;
-      if (i < rows * VPR) {
-        const int r = blk * kGroup + i / VPR, c = i % VPR;
-        kv[j] = *(const uint4*)(krow(D + r) + c * 8);
-        vv[j] = *(const uint4*)(vrow(D + r) + c * 8);
+      for (int j = 0; j < kPer; ++j) {
+        const int i = tid + j * kWriterThreads;
+        if (i < rows * VPR) {
+          const int r = r_base + i / VPR, c = i % VPR;
+          shk[j] = *(const w4*)(krow(D + r) + c * 8);
+          shv[j] = *(const w4*)(vrow(D + r) + c * 8);
+        }
       }
+      __syncthreads();  // this pass's loads, in every thread, before its stores
+    } else {
+      // the first pass's sources were waited for before the first barrier;
+      // the aged-group reads of every thread finished before their LDS
+      // barriers, so only arrival is needed here
+      lds_barrier();
     }
-    // Sources of this block never overlap its destinations (D >= 32), but the
-    // previous block's sources may be this block's destinations.
-    __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kPer; ++j) {
       const int i = tid + j * kWriterThreads;
       if (i < rows * VPR) {
-        const int r = blk * kGroup + i / VPR, c = i % VPR;
-        *(uint4*)(ks + (int64_t)r * HD + c * 8) = kv[j];
-        *(uint4*)(vs + (int64_t)r * HD + c * 8) = vv[j];
+        const int r = r_base + i / VPR, c = i % VPR;
+        *(w4*)(ks + (int64_t)r * HD + c * 8) = shk[j];
+        *(w4*)(vs + (int64_t)r * HD + c * 8) = shv[j];
       }
     }
   }

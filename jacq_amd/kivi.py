@@ -132,6 +132,8 @@ def lib() -> ctypes.CDLL:
     L.jacq_kivi_profile_stop.argtypes = [ctypes.POINTER(ctypes.c_float),
                                          ctypes.POINTER(ctypes.c_float), _i32]
     L.jacq_kivi_profile_stop.restype = _i32
+    L.jacq_kivi_profile_write_ms.argtypes = [ctypes.POINTER(ctypes.c_float), _i32]
+    L.jacq_kivi_profile_write_ms.restype = _i32
     _lib = L
     return L
 
@@ -154,6 +156,15 @@ def profile_stop(cap: int = 4096):
     if n < 0:
         raise KiviLaunchError(last_error())
     return list(k[:n]), list(m[:n])
+
+
+def profile_write_ms(cap: int = 4096):
+    """Cache-write kernel ms per call recorded in the last profiling window."""
+    w = (ctypes.c_float * cap)()
+    n = lib().jacq_kivi_profile_write_ms(w, cap)
+    if n < 0:
+        raise KiviLaunchError(last_error())
+    return list(w[:n])
 
 
 def _ptr(t: torch.Tensor | None):

@@ -73,7 +73,8 @@ def test_header_declares_the_reference_symbols():
         "jacq_kivi_abi_version", "jacq_kivi_ext_version", "jacq_kivi_last_error",
         "jacq_kivi_check_geometry", "jacq_kivi_max_seq_len", "jacq_kivi_check_block_table_width",
         "jacq_kivi_decode_workspace_size", "jacq_kivi_decode", "jacq_kivi_cache_append",
-        "jacq_kivi_plan_batched_write", "jacq_kivi_profile_start", "jacq_kivi_profile_stop"])
+        "jacq_kivi_plan_batched_write", "jacq_kivi_profile_start", "jacq_kivi_profile_stop",
+        "jacq_kivi_profile_write_ms"])
 
 
 def test_library_exports_every_declared_function(native):
