@@ -10,6 +10,7 @@
 #include <climits>
 #include <cstdio>
 #include <cstdlib>
+#include <initializer_list>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -198,6 +199,15 @@ void profile_write_slot(hipEvent_t out[2]) {
   ++g_prof.wused;
 }
 
+// The kernels move Q, O, codes, scales, scratch and new tokens in 16-byte
+// vectors (and the workspace in float4), so every base address must be
+// 16-byte aligned; torch allocations and their row slices are.
+static bool aligned16(std::initializer_list<const void*> ps) {
+  uintptr_t bits = 0;
+  for (const void* p : ps) bits |= (uintptr_t)p;
+  return (bits & 15u) == 0;
+}
+
 // Decode with a runtime geometry; seq_len_host >= 0 when the (single) length
 // is known on the host, which tightens the split plan.
 int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t* seq_lens,
@@ -206,6 +216,8 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
                const jacq_half_t* vsc, const jacq_half_t* vz, const jacq_half_t* kscr,
                const jacq_half_t* vscr, int64_t scr_stride, int batch, float* O, void* ws,
                size_t ws_bytes, hipStream_t stream) {
+  if (!aligned16({Q, O, kc, ksc, kz, vc, vsc, vz, kscr, vscr, ws}))
+    return fail(JACQ_KIVI_EINVAL, "tensor and workspace pointers must be 16-byte aligned");
   const KiviGeo g = make_geo(x);
   int dev = 0;
   if (int e = current_device(&dev)) return e;
@@ -265,6 +277,8 @@ int run_append(const jacq_kivi_geometry& x, uint8_t* kc, jacq_half_t* ksc, jacq_
                const jacq_half_t* nv, int64_t new_stride, const int32_t* bt, int64_t bt_stride,
                const int32_t* start_lens, int start_len, int num_new, int batch,
                hipStream_t stream) {
+  if (!aligned16({kc, ksc, kz, vc, vsc, vz, kscr, vscr, nk, nv}))
+    return fail(JACQ_KIVI_EINVAL, "tensor pointers must be 16-byte aligned");
   const KiviGeo g = make_geo(x);
   jacq::AppendArgs a{};
   a.k_code = kc;

@@ -484,6 +484,7 @@ template <int HD>
 struct SegCtx {
   half8_t qn[HD / 32];  // B operand of Q, natural channel order (bias, residual tiles)
   half8_t qp[HD / 32];  // B operand of Q in the unpack order, odd channels / 16
+  half8_t qm[HD / 32];  // packed mode: qp in columns 8-15 (lo), zero in columns 0-7 (hi)
 };
 
 // QK^T of one quantised group (already in LDS) and its online-softmax update:
@@ -507,16 +508,15 @@ __device__ inline half8_t qk_softmax(WaveState<HD>& st, const SegCtx<HD>& q,
     // G <= 8: columns 0-7 carry q*s (hi) of heads 0-7, columns 8-15 the
     // rounding remainder (lo) of the same heads, so one MFMA does both; a
     // row_ror:8 add merges the halves (and leaves the sum in both lanes).
-    const bool hi_col = (lane & 15) < 8;
+    // fma(q, s, -(qm * s)): round(q * s) where qm = 0 (hi), the exact
+    // remainder q * s - round(q * s) where qm = q (lo)
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const uint8_t* kp = &buf->s[2 * (j * (HD / 4) + 8 * ks)];
       const u32x4 sv = *(const u32x4*)kp;
       const u32x4 zv = *(const u32x4*)(kp + 2 * HD);
       const half8_t sp = as_h8(perm_pairs(sv));
-      const half8_t qs = q.qp[ks] * sp;
-      const half8_t ql = __builtin_elementwise_fma(q.qp[ks], sp, -qs);
-      const half8_t bq = hi_col ? qs : ql;
+      const half8_t bq = __builtin_elementwise_fma(q.qp[ks], sp, -(q.qm[ks] * sp));
       bz = mfma(as_h8(zv), q.qn[ks], bz);  // sum_d z_d q_gd
       bh = mfma(neg1024, bq, bh);           // -1024 sum_d B_gd (hi | lo)
       s0 = mfma(as_h8(unpack_codes(kc[0][ks], nb)), bq, s0);
@@ -736,6 +736,7 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
       const half8_t div = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)0.0625f, (_Float16)0.0625f,
                            (_Float16)1.0f, (_Float16)1.0f, (_Float16)0.0625f, (_Float16)0.0625f};
       q.qp[ks] = as_h8(perm_pairs(v)) * div;
+      q.qm[ks] = (PACK && c >= 8) ? q.qp[ks] : half8_t(0);
     }
     WaveState<HD> st;
 #pragma unroll
@@ -853,48 +854,64 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
 // segment that one wavefront finished costs a single scalar load here, and a
 // cut one loads all of its partials at once.
 __global__ __launch_bounds__(256) void kivi_combine_stream_kernel(KiviGeo g, DecodeArgs a) {
-  constexpr int K = 8;  // outputs per thread: G * HD <= 16 * 128
+  constexpr int K = 2;  // float4 outputs per thread: G * HD <= 16 * 128 = 2048 = 256 * K * 4
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int G = g.gqa, HD = g.hd, NKV = g.nkv, n = G * HD;
+  const int G = g.gqa, HD = g.hd, NKV = g.nkv, n4 = G * HD / 4;
   const int64_t seg = (int64_t)b * NKV + h;
   const __attribute__((address_space(4))) int32_t* sw =
       (const __attribute__((address_space(4))) int32_t*)a.ws_seg;
   const int w0 = sw[2 * seg], w1 = sw[2 * seg + 1];
   if (w0 >= w1) return;  // written whole by the decode kernel
   int gi[K], d[K];
-  float M[K], L[K], acc[K];
+  bool on[K];
+  floatx4 acc[K];
+  float M[K], L[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    const int e = min(tid + 256 * k, n - 1);
-    gi[k] = e / HD;
-    d[k] = e - gi[k] * HD;
+    const int e = tid + 256 * k;  // outputs 4e .. 4e + 3 of one head (HD % 4 == 0)
+    on[k] = e < n4;
+    gi[k] = 4 * e / HD;
+    d[k] = 4 * e - gi[k] * HD;
     M[k] = -INFINITY;
     L[k] = 0.0f;
-    acc[k] = 0.0f;
+    acc[k] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
-  // every load of one partial is issued before the first is used
-  for (int w = w0; w <= w1; ++w) {
-    float m[K], l[K], v[K];
+  // the loads of U partials are issued before the first is used: a segment's
+  // few partials cost one or two memory latencies, not one each
+  constexpr int U = 4;
+  for (int w = w0; w <= w1; w += U) {
+    float2 ml[U][K];
+    floatx4 v[U][K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int64_t p = (seg + w) * G + gi[k];
-      m[k] = a.ws_ml[2 * p];
-      l[k] = a.ws_ml[2 * p + 1];
-      v[k] = a.ws_acc[p * HD + d[k]];
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        ml[u][k] = float2{-INFINITY, 0.0f};  // past the end: folded with weight 0
+        v[u][k] = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (on[k] && w + u <= w1) {
+          const int64_t p = (seg + w + u) * G + gi[k];
+          ml[u][k] = *(const float2*)(a.ws_ml + 2 * p);
+          v[u][k] = *(const floatx4*)(a.ws_acc + p * HD + d[k]);
+        }
+      }
     }
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const float mn = fmaxf(M[k], m[k]);
-      const float fo = __builtin_amdgcn_exp2f(M[k] - mn), fn = __builtin_amdgcn_exp2f(m[k] - mn);
-      acc[k] = acc[k] * fo + v[k] * fn;
-      L[k] = L[k] * fo + l[k] * fn;
-      M[k] = mn;
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const float mn = fmaxf(M[k], ml[u][k].x);
+        const float fo = __builtin_amdgcn_exp2f(M[k] - mn);
+        const float fn = __builtin_amdgcn_exp2f(ml[u][k].x - mn);
+        acc[k] = acc[k] * fo + v[u][k] * fn;
+        L[k] = L[k] * fo + ml[u][k].y * fn;
+        M[k] = mn;
+      }
     }
   }
   float* out = a.out + (int64_t)b * a.out_stride + (int64_t)h * G * HD;
 #pragma unroll
   for (int k = 0; k < K; ++k)
-    if (tid + 256 * k < n) out[(int64_t)gi[k] * HD + d[k]] = acc[k] / fmaxf(L[k], 1.0e-30f);
+    if (on[k]) *(floatx4*)(out + (int64_t)gi[k] * HD + d[k]) = acc[k] / fmaxf(L[k], 1.0e-30f);
 }
 
 template <int HD, int P>

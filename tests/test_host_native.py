@@ -274,3 +274,18 @@ int main(int argc, char**) {
              ["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", "-o",
               str(tmp_path / "binding"), f"-L{lib_dir}", "-ljacq_kivi", "-Wl,--no-as-needed",
               f"-Wl,-rpath,{lib_dir}", "-L/opt/rocm/lib", "-lamdhip64"])
+
+
+def test_runtime_entry_points_reject_unaligned_pointers(native):
+    """Both runtime entry points refuse a base address that is not 16-byte
+    aligned before any HIP call (the kernels move 16-byte vectors)."""
+    g = geo()
+    ok, odd = 1 << 20, (1 << 20) + 2
+    decode = [ok] * 11
+    decode[0] = odd  # Q offset by one fp16 element
+    assert native.jacq_kivi_decode(ctypes.byref(g), *decode, 1, ok, None, 0, None) == 1
+    assert b"16-byte aligned" in native.jacq_kivi_last_error()
+    append = [ok] * 12
+    append[8] = odd  # NEW_K
+    assert native.jacq_kivi_cache_append(ctypes.byref(g), *append, 1, 1, None) == 1
+    assert b"16-byte aligned" in native.jacq_kivi_last_error()
