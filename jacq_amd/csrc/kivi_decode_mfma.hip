@@ -56,6 +56,7 @@ __device__ inline half8_t as_h8(u32x4 v) { return __builtin_bit_cast(half8_t, v)
 __device__ inline u32x4 as_u4(half8_t v) { return __builtin_bit_cast(u32x4, v); }
 __device__ inline half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
 __device__ inline uint32_t as_u(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ inline _Float16 as_f16(uint16_t v) { return __builtin_bit_cast(_Float16, v); }
 
 // Bit constants of the nibble -> fp16 conversion, held in registers so that
 // mask-and-merge is one v_and_or_b32 (VOP3 takes no literal operands here).
@@ -121,11 +122,30 @@ __device__ constexpr int tok_k(int tt, int c) {
 }
 __device__ constexpr int tok_v(int j, int e) { return 2 * e + (j & 1) + 16 * (j >> 1); }
 
+template <int HD>
+struct StageBuf {
+  uint8_t k[32 * HD / 2];
+  uint8_t v[32 * HD / 2];
+  uint8_t s[4 * HD + 128 * (HD / kGroup)];
+  uint8_t ones[128];  // fp16 1.0, written once: the row-sum lanes read it as V zeros
+};
+
+// The lanes whose column of the Sigma P z tile carries Sigma P: the last
+// column of each 32-channel group (lane c covers channels CPL*c ..).
+template <int HD>
+__device__ inline bool sum_lane(int c) {
+  constexpr int per = kGroup / (HD / 16);  // columns per V group
+  return c % per == per - 1;
+}
+
 // Per-lane LDS read offsets inside a stage, fixed for the whole kernel.
 struct LaneMap {
   int kread[2];  // K codes of tile tt: row tok_k(tt, c), channel block j
   int vread;     // V codes: row tok_v(j, 0), channels CPL*c..; element e adds 2e rows
   int vsread;    // V scale of (token tok_v(j, 0), group of channel CPL*c)
+  int vzread;    // V zeros of the same (from the stage start); the ones block in
+                 // the last lane of each group's columns, whose Sigma P z column
+                 // then carries the row sum Sigma P instead
 };
 
 template <int HD, int P>
@@ -137,6 +157,8 @@ __device__ inline LaneMap lane_map(int lane) {
   for (int tt = 0; tt < 2; ++tt) m.kread[tt] = tok_k(tt, c) * C::HDP + j * C::KCB;
   m.vread = tok_v(j, 0) * C::HDP + c * (C::CPL / 2);
   m.vsread = 2 * (tok_v(j, 0) * C::HDG + (C::CPL * c) / kGroup);
+  m.vzread = sum_lane<HD>(c) ? (int)offsetof(StageBuf<HD>, ones)
+                             : (int)offsetof(StageBuf<HD>, s) + 4 * HD + m.vsread + 64 * C::HDG;
   return m;
 }
 
@@ -150,12 +172,6 @@ __device__ inline LaneMap lane_map(int lane) {
 // whatever its width, so a group is 2 * 32*HD/2 / 1024 + 1 of them.  The DMAs
 // are issued from inline asm and waited for with explicit vmcnt counts: a
 // ring of stages keeps S - 1 groups in flight while one is computed.
-template <int HD>
-struct StageBuf {
-  uint8_t k[32 * HD / 2];
-  uint8_t v[32 * HD / 2];
-  uint8_t s[4 * HD + 128 * (HD / kGroup)];
-};
 
 template <int HD>
 constexpr int code_dmas() {  // 1 KiB DMAs per K or V code block
@@ -333,9 +349,8 @@ __device__ inline float max_xor32(float x) {
 template <int HD>
 struct WaveState {
   floatx4 o[HD / 16];  // O tiles: lane holds O[4j+i][CPL*c + nt]
-  floatx4 ob;          // sum_t P z_t: applies to every channel of lane c
+  floatx4 ob;          // sum_t P z_t of lane c's group; sum_t P in the sum lanes
   float m;             // running max (log2 domain) of head c
-  float l;             // this lane's share of the running denominator
 };
 
 template <int HD>
@@ -350,7 +365,6 @@ __device__ inline void rescale(WaveState<HD>& st, float corr, int j) {
     for (int i = 0; i < 4; ++i) st.o[nt][i] *= ci[i];
 #pragma unroll
   for (int i = 0; i < 4; ++i) st.ob[i] *= ci[i];
-  st.l *= corr;
 }
 
 // Online-softmax update for raw scores s[tt][i] of tokens 8j + 4tt + i and
@@ -379,13 +393,8 @@ __device__ inline half8_t softmax_tile(WaveState<HD>& st, floatx4 s0, floatx4 s1
     p[4 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], kscale, off));
   }
   half8_t pa;
-  float sum = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    sum += p[i];
-    pa[i] = (_Float16)p[i];
-  }
-  st.l += sum;
+  for (int i = 0; i < 8; ++i) pa[i] = (_Float16)p[i];
   return pa;
 }
 
@@ -411,12 +420,13 @@ __device__ inline VData load_v(const StageBuf<HD>* buf, const LaneMap& lm) {
       d.vc[e] = *(const uint16_t*)vp;
   }
   const uint8_t* vp = &buf->s[4 * HD + lm.vsread];
+  const uint8_t* zp = (const uint8_t*)buf + lm.vzread;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {  // pair q = e: tokens two rows apart
     const uint8_t* p0 = vp + 8 * HDG * e;
+    const uint8_t* z0 = zp + 8 * HDG * e;
     d.vs4[e] = (uint32_t)*(const uint16_t*)p0 | ((uint32_t)*(const uint16_t*)(p0 + 4 * HDG) << 16);
-    d.vz4[e] = (uint32_t)*(const uint16_t*)(p0 + 64 * HDG) |
-               ((uint32_t)*(const uint16_t*)(p0 + 64 * HDG + 4 * HDG) << 16);
+    d.vz4[e] = (uint32_t)*(const uint16_t*)z0 | ((uint32_t)*(const uint16_t*)(z0 + 4 * HDG) << 16);
   }
   return d;
 }
@@ -424,34 +434,36 @@ __device__ inline VData load_v(const StageBuf<HD>* buf, const LaneMap& lm) {
 // |s| >= 64 somewhere in the wave's V scales (fp16 exponent field >= 0x15).
 // The OR of the bit patterns reaches the bound whenever one value does (and,
 // rarely, when none does, which only selects the slower exact arithmetic).
-__device__ inline bool big_scales(const VData& d) {
+__device__ inline uint64_t big_scales(const VData& d) {
   const uint32_t sor = (d.vs4[0] | d.vs4[1] | d.vs4[2] | d.vs4[3]) & 0x7FFF7FFFu;
   const bool big = (sor & 0xFFFFu) >= 0x5400u || sor >= 0x54000000u;
-  return __builtin_amdgcn_ballot_w64(big) != 0;
+  return __builtin_amdgcn_ballot_w64(big);  // nonzero: some lane holds a big scale
 }
 
 // PV of one group, dequantising the lane's V channels CPL*c + 2k (low
 // nibbles) and + 2k + 1 (high nibbles) for its 8 tokens.  x = 1024 + code is
 // exact in fp16, so code * s = fma(x, s, -1024 s) with one rounding; the high
 // nibble carries 16x and uses s / 16.  When some |s| >= 64 (`big`,
-// wave-uniform) -1024 s and even code * s can leave the fp16 range: then x -
-// 1024 = code is formed first (exact), the products use s / 128 with a zero
+// wave-uniform) -1024 s and even code * s can leave the fp16 range: then
+// x / 128 - 8 = code / 128 is formed first (exact), the products take a zero
 // addend and P carries the 128 back (powers of two: exact; P stays below
 // 2^15).  Both cases share one instruction stream and its registers.
 template <int HD>
 __device__ inline void pv_group(WaveState<HD>& st, half8_t pa, const VData& d, const Nibble& nb,
-                                bool big) {
+                                uint64_t bigmask) {
   constexpr int CPL = HD / 16;
   const half8_t sv = as_h8(d.vs4);
-  const _Float16 f_lo = big ? (_Float16)(1.0f / 128.0f) : (_Float16)1.0f;
-  const _Float16 f_hi = big ? (_Float16)(1.0f / 2048.0f) : (_Float16)0.0625f;
-  const _Float16 f_n = big ? (_Float16)0.0f : (_Float16)-1024.0f;
-  const _Float16 f_p = big ? (_Float16)128.0f : (_Float16)1.0f;
-  const half8_t slo = sv * f_lo, shi = sv * f_hi;
-  const u32x4 s_lo = as_u4(slo), s_hi = as_u4(shi);
-  const u32x4 n_lo = as_u4(slo * f_n), n_hi = as_u4(shi * f_n);  // -1024 s (exact) or 0
+  // wave-uniform constants chosen by scalar selects on the ballot mask
+  const bool big = bigmask != 0;
+  const uint32_t fn2 = __builtin_amdgcn_readfirstlane(big ? 0u : 0xE400E400u);   // 0 or -1024
+  const uint32_t fp2 = __builtin_amdgcn_readfirstlane(big ? 0x58005800u : 0x3C003C00u);  // 128 or 1
+  const _Float16 f_n = as_h2(fn2)[0], f_p = as_h2(fp2)[0];
+  const half8_t shi = sv * (_Float16)0.0625f;
+  const u32x4 s_lo = d.vs4, s_hi = as_u4(shi);
+  const u32x4 n_lo = as_u4(sv * f_n), n_hi = as_u4(shi * f_n);  // -1024 s (exact) or 0
   const half8_t pv = pa * f_p;
-  const half2_t m1024_2 = {(_Float16)-1024.f, (_Float16)-1024.f};
+  const half2_t r128_2 = {(_Float16)(1.0f / 128.0f), (_Float16)(1.0f / 128.0f)};
+  const half2_t m8_2 = {(_Float16)-8.f, (_Float16)-8.f};
 #pragma unroll
   for (int k = 0; k < CPL / 2; ++k) {
     uint32_t xl[4], xh[4];
@@ -464,8 +476,8 @@ __device__ inline void pv_group(WaveState<HD>& st, half8_t pa, const VData& d, c
     if (__builtin_expect(big, 0)) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        xl[q] = as_u(as_h2(xl[q]) + m1024_2);
-        xh[q] = as_u(as_h2(xh[q]) + m1024_2);
+        xl[q] = as_u(__builtin_elementwise_fma(as_h2(xl[q]), r128_2, m8_2));  // code / 128
+        xh[q] = as_u(__builtin_elementwise_fma(as_h2(xh[q]), r128_2, m8_2));  // code / 8
       }
     }
     u32x4 lo, hi;
@@ -510,17 +522,24 @@ __device__ inline half8_t qk_softmax(WaveState<HD>& st, const SegCtx<HD>& q,
     // row_ror:8 add merges the halves (and leaves the sum in both lanes).
     // fma(q, s, -(qm * s)): round(q * s) where qm = 0 (hi), the exact
     // remainder q * s - round(q * s) where qm = q (lo)
+    half8_t bq[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const uint8_t* kp = &buf->s[2 * (j * (HD / 4) + 8 * ks)];
       const u32x4 sv = *(const u32x4*)kp;
       const u32x4 zv = *(const u32x4*)(kp + 2 * HD);
       const half8_t sp = as_h8(perm_pairs(sv));
-      const half8_t bq = __builtin_elementwise_fma(q.qp[ks], sp, -(q.qm[ks] * sp));
+      bq[ks] = __builtin_elementwise_fma(q.qp[ks], sp, -(q.qm[ks] * sp));
       bz = mfma(as_h8(zv), q.qn[ks], bz);  // sum_d z_d q_gd
-      bh = mfma(neg1024, bq, bh);           // -1024 sum_d B_gd (hi | lo)
-      s0 = mfma(as_h8(unpack_codes(kc[0][ks], nb)), bq, s0);
-      s1 = mfma(as_h8(unpack_codes(kc[1][ks], nb)), bq, s1);
+      bh = mfma(neg1024, bq[ks], bh);       // -1024 sum_d B_gd (hi | lo)
+    }
+    // the bias is added before the hi/lo merge: a DPP add whose source is an
+    // MFMA result register is miscompiled (the DPP combiner reads the
+    // tuple's first register for every element), one on a VALU result is not
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      s0 = mfma(as_h8(unpack_codes(kc[0][ks], nb)), bq[ks], s0);
+      s1 = mfma(as_h8(unpack_codes(kc[1][ks], nb)), bq[ks], s1);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -686,9 +705,32 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
 
   const Nibble nb;
   const LaneMap lm = lane_map<HD, P>(lane);
+  const bool sum_col = sum_lane<HD>(c);
+  constexpr int C1 = kGroup / CPL - 1;  // a sum column (the first group's)
+  // the ones block of every stage (the DMAs never write it)
+  if (lane < 32) {
+#pragma unroll
+    for (int s_ = 0; s_ < S; ++s_) ((uint32_t*)ring[s_].ones)[lane] = 0x3C003C00u;
+  }
   const float sscale = 1.4426950408889634f / __builtin_sqrtf((float)HD);  // log2(e)/sqrt(HD)
   const int which = lane >> 5, t32 = lane & 31;
 
+  // Issue arbitration favours the older of a SIMD's two waves, which left
+  // alone finishes its run well before the younger.  Each wave drops its
+  // priority at every quarter of its own run, so a wave behind its partner
+  // outranks it and the pair ends closer together.
+  const int n_run = (int)(x1 - x0), q1 = n_run / 4, q2 = n_run / 2, q3 = 3 * n_run / 4;
+  int done = 0;
+  __builtin_amdgcn_s_setprio(3);
+  auto progress = [&]() {
+    ++done;
+    if (done == q1)
+      __builtin_amdgcn_s_setprio(2);
+    else if (done == q2)
+      __builtin_amdgcn_s_setprio(1);
+    else if (done == q3)
+      __builtin_amdgcn_s_setprio(0);
+  };
   SeqSpan sp = locate(g, a, x0, lane);
   int kvh = (int)((x0 - sp.start) / sp.tiles);
   int t = (int)((x0 - sp.start) % sp.tiles);
@@ -743,7 +785,6 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
     for (int nt = 0; nt < CPL; ++nt) st.o[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
     st.ob = floatx4{0.f, 0.f, 0.f, 0.f};
     st.m = -1.0e30f;
-    st.l = 0.0f;
 
     const int r_beg = max(t_beg, ov / kGroup);  // first fp16 residual tile
     if (t_beg < tq_end) {
@@ -765,6 +806,7 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
         st.ob = mfma(pa, as_h8(vd.vz4), st.ob);  // sum_t P z_t
         pv_group<HD>(st, pa, vd, nb, big_scales(vd));
         slot = slot == S - 1 ? 0 : slot + 1;
+        progress();
       }
     }
 
@@ -798,18 +840,23 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
         }
         st.o[nt] = mfma(pr, as_h8(vb), st.o[nt]);
       }
+      // Sigma P into the sum columns (the fp16 tokens carry no zero point)
+      const uint32_t one2 = sum_col ? 0x3C003C00u : 0u;
+      st.ob = mfma(pr, as_h8(u32x4{one2, one2, one2, one2}), st.ob);
+      progress();
     }
 
     // ---- segment output: O directly, or a partial for the combine kernel ----
-    float lsum = st.l;
-    lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);
+    // row sums: Sigma P of O row 4j + i sits in the sum column C1 of row
+    // block j; a sum lane takes its group's Sigma P z from its left neighbour
     const bool whole = (t_beg == 0 && t_fin == T);
     const int64_t piece = (int64_t)b * NKV + h + w;
-    float rowscale[4];
+    float rowscale[4], zsum[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float li = __shfl(lsum, 4 * j + i, 64);
+      const float li = __shfl(st.ob[i], 16 * j + C1, 64);
+      const float left = __shfl(st.ob[i], lane - 1, 64);
+      zsum[i] = sum_col ? left : st.ob[i];
       rowscale[i] = whole ? 1.0f / fmaxf(li, 1.0e-30f) : 1.0f;
     }
     float* dst = whole ? a.out + (int64_t)b * a.out_stride + (int64_t)h * G * HD
@@ -820,16 +867,20 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
       if (row < G) {
         float v[CPL];
 #pragma unroll
-        for (int nt = 0; nt < CPL; ++nt) v[nt] = (st.o[nt][i] + st.ob[i]) * rowscale[i];
+        for (int nt = 0; nt < CPL; ++nt) v[nt] = (st.o[nt][i] + zsum[i]) * rowscale[i];
         float* p = dst + (int64_t)row * HD + CPL * c;
 #pragma unroll
         for (int q4 = 0; q4 < CPL / 4; ++q4)
           *(floatx4*)(p + 4 * q4) = floatx4{v[4 * q4], v[4 * q4 + 1], v[4 * q4 + 2], v[4 * q4 + 3]};
       }
     }
+    float lh[4];  // Sigma P of head c (rows 4 (c >> 2) + i)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lh[i] = __shfl(st.ob[i], 16 * (c >> 2) + C1, 64);
     if (!whole && j == 0 && c < G) {
+      const int ci = c & 3;
       a.ws_ml[(piece * G + c) * 2] = st.m;
-      a.ws_ml[(piece * G + c) * 2 + 1] = lsum;
+      a.ws_ml[(piece * G + c) * 2 + 1] = ci == 0 ? lh[0] : ci == 1 ? lh[1] : ci == 2 ? lh[2] : lh[3];
     }
     if (lane == 0) {  // the combine kernel's map: first and last wavefront of the segment
       const int64_t seg = (int64_t)b * NKV + h;
