@@ -80,6 +80,30 @@ void jac_launch_tp2_local(const jacq_half_t* Q, const int32_t* BLOCK_TABLE,
                           const jacq_half_t* V_RESIDUAL_SCRATCH, int SEQ_LEN, float* O,
                           hipStream_t stream);
 
+/* Sparse-retained decode: the old tokens come from the first
+ * NUM_RETAINED_PAGES entries of the compact RETAINED_BLOCK_TABLE (clamped to
+ * the dense old pages of SEQ_LEN), the residual window from the scratch at the
+ * dense SEQ_LEN boundary.  Replaces jac_launch_sparse_retained,
+ * crates/jac-codegen-cuda/src/variants.rs:2620-2740 (declared at
+ * integrations/vllm_kivi/source_patch.py:589-595). */
+void jac_launch_sparse_retained(const jacq_half_t* Q, const int32_t* RETAINED_BLOCK_TABLE,
+                                const uint8_t* K_CODE_PAGES, const jacq_half_t* K_SCALE_PAGES,
+                                const jacq_half_t* K_ZERO_PAGES, const uint8_t* V_CODE_PAGES,
+                                const jacq_half_t* V_SCALE_PAGES,
+                                const jacq_half_t* V_ZERO_PAGES,
+                                const jacq_half_t* K_RESIDUAL_SCRATCH,
+                                const jacq_half_t* V_RESIDUAL_SCRATCH, int SEQ_LEN,
+                                int NUM_RETAINED_PAGES, float* O, hipStream_t stream);
+
+/* source_patch.py:597-603. */
+void jac_launch_sparse_retained_tp2_local(
+    const jacq_half_t* Q, const int32_t* RETAINED_BLOCK_TABLE, const uint8_t* K_CODE_PAGES,
+    const jacq_half_t* K_SCALE_PAGES, const jacq_half_t* K_ZERO_PAGES,
+    const uint8_t* V_CODE_PAGES, const jacq_half_t* V_SCALE_PAGES,
+    const jacq_half_t* V_ZERO_PAGES, const jacq_half_t* K_RESIDUAL_SCRATCH,
+    const jacq_half_t* V_RESIDUAL_SCRATCH, int SEQ_LEN, int NUM_RETAINED_PAGES, float* O,
+    hipStream_t stream);
+
 /* NUM_QUERIES (<= 160) queries of ONE sequence, query i attending to the
  * first SEQ_LENS[i] tokens; Q/O [NUM_QUERIES,NH,HD].  Replaces
  * jac_launch_batched, crates/jac-codegen-cuda/src/variants.rs:2776-2930
@@ -210,6 +234,26 @@ int jacq_kivi_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q,
                      const jacq_half_t* K_RESIDUAL_SCRATCH,
                      const jacq_half_t* V_RESIDUAL_SCRATCH, int32_t batch, float* O,
                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Sparse-retained decode of one sequence at a runtime geometry (the
+ * jac_launch_sparse_retained window, variants.rs:2667-2680).
+ *   Q                     [NH, HD] fp16
+ *   RETAINED_BLOCK_TABLE  compact physical-page ids of the retained old pages
+ *   K/V_SCR               [NKV, R+32, HD] fp16
+ *   O                     [NH, HD] fp32
+ * NUM_RETAINED_PAGES must be in [0, max_pages_per_seq] and <= num_pages, and
+ * SEQ_LEN in [1, jacq_kivi_max_seq_len] (the checks of source_patch.py:942-945
+ * at this geometry); the device clamps NUM_RETAINED_PAGES to the dense old
+ * pages of SEQ_LEN.  At page 16 the retained pages are taken in whole 32-token
+ * groups.  workspace as for jacq_kivi_decode (batch 1). */
+int jacq_kivi_decode_sparse_retained(
+    const jacq_kivi_geometry* geo, const jacq_half_t* Q, int32_t SEQ_LEN,
+    const int32_t* RETAINED_BLOCK_TABLE, int32_t NUM_RETAINED_PAGES,
+    const uint8_t* K_CODE_PAGES, const jacq_half_t* K_SCALE_PAGES,
+    const jacq_half_t* K_ZERO_PAGES, const uint8_t* V_CODE_PAGES,
+    const jacq_half_t* V_SCALE_PAGES, const jacq_half_t* V_ZERO_PAGES,
+    const jacq_half_t* K_RESIDUAL_SCRATCH, const jacq_half_t* V_RESIDUAL_SCRATCH, float* O,
+    void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Append num_new tokens to each of `batch` sequences in one launch.
  *   NEW_K/NEW_V   [batch, num_new, NKV, HD] fp16, token-major per sequence

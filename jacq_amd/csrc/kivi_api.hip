@@ -209,13 +209,14 @@ static bool aligned16(std::initializer_list<const void*> ps) {
 }
 
 // Decode with a runtime geometry; seq_len_host >= 0 when the (single) length
-// is known on the host, which tightens the split plan.
+// is known on the host, which tightens the split plan.  retained_pages >= 0
+// selects the sparse-retained window (bt is then the compact table).
 int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t* seq_lens,
                int seq_len_host, const int32_t* bt, int64_t bt_stride, const uint8_t* kc,
                const jacq_half_t* ksc, const jacq_half_t* kz, const uint8_t* vc,
                const jacq_half_t* vsc, const jacq_half_t* vz, const jacq_half_t* kscr,
                const jacq_half_t* vscr, int64_t scr_stride, int batch, float* O, void* ws,
-               size_t ws_bytes, hipStream_t stream) {
+               size_t ws_bytes, hipStream_t stream, int retained_pages = -1) {
   if (!aligned16({Q, O, kc, ksc, kz, vc, vsc, vz, kscr, vscr, ws}))
     return fail(JACQ_KIVI_EINVAL, "tensor and workspace pointers must be 16-byte aligned");
   const KiviGeo g = make_geo(x);
@@ -224,7 +225,7 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
   int64_t max_tokens = max_seq_len(x);
   if (seq_len_host >= 0) {
     int ov, rv;
-    jacq::decode_window(g, seq_len_host, &ov, &rv);
+    jacq::window_of(g, retained_pages, seq_len_host, &ov, &rv);
     max_tokens = ov + rv;
   }
   const SplitPlan sp = plan_splits(max_tokens);
@@ -257,6 +258,7 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
   a.scr_stride = scr_stride;
   a.out = O;
   a.out_stride = (int64_t)g.nh * g.hd;
+  a.retained_pages = retained_pages;
   fill_ws(a, g, batch, sp, waves, need > 0 ? ws : nullptr);
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   profile_slot(ev);
@@ -377,6 +379,36 @@ int jacq_kivi_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q, const 
                     K_SCALE_PAGES, K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES,
                     K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, scr, batch, O, workspace,
                     workspace_bytes_, stream);
+}
+
+int jacq_kivi_decode_sparse_retained(
+    const jacq_kivi_geometry* geo, const jacq_half_t* Q, int32_t SEQ_LEN,
+    const int32_t* RETAINED_BLOCK_TABLE, int32_t NUM_RETAINED_PAGES,
+    const uint8_t* K_CODE_PAGES, const jacq_half_t* K_SCALE_PAGES,
+    const jacq_half_t* K_ZERO_PAGES, const uint8_t* V_CODE_PAGES,
+    const jacq_half_t* V_SCALE_PAGES, const jacq_half_t* V_ZERO_PAGES,
+    const jacq_half_t* K_RESIDUAL_SCRATCH, const jacq_half_t* V_RESIDUAL_SCRATCH, float* O,
+    void* workspace, size_t workspace_bytes_, hipStream_t stream) {
+  if (int e = check_geometry(geo)) return e;
+  if (NUM_RETAINED_PAGES < 0 || NUM_RETAINED_PAGES > geo->max_pages_per_seq)
+    return fail(JACQ_KIVI_EINVAL, "NUM_RETAINED_PAGES must be in [0, max_pages_per_seq = " +
+                                      std::to_string(geo->max_pages_per_seq) + "], got " +
+                                      std::to_string(NUM_RETAINED_PAGES));
+  if (NUM_RETAINED_PAGES > geo->num_pages)
+    return fail(JACQ_KIVI_EINVAL,
+                "NUM_RETAINED_PAGES cannot exceed physical page storage capacity");
+  const int64_t cap = max_seq_len(*geo);
+  if (SEQ_LEN < 1 || SEQ_LEN > cap)
+    return fail(JACQ_KIVI_EINVAL, "SEQ_LEN must be in [1, " + std::to_string(cap) + "], got " +
+                                      std::to_string(SEQ_LEN));
+  if (!Q || !K_CODE_PAGES || !K_SCALE_PAGES || !K_ZERO_PAGES || !V_CODE_PAGES ||
+      !V_SCALE_PAGES || !V_ZERO_PAGES || !K_RESIDUAL_SCRATCH || !V_RESIDUAL_SCRATCH || !O ||
+      (!RETAINED_BLOCK_TABLE && NUM_RETAINED_PAGES > 0))
+    return fail(JACQ_KIVI_EINVAL, "null tensor pointer");
+  return run_decode(*geo, Q, nullptr, SEQ_LEN, RETAINED_BLOCK_TABLE, 0, K_CODE_PAGES,
+                    K_SCALE_PAGES, K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES,
+                    K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, 0, 1, O, workspace,
+                    workspace_bytes_, stream, NUM_RETAINED_PAGES);
 }
 
 int jacq_kivi_cache_append(const jacq_kivi_geometry* geo, uint8_t* K_CODE_PAGES,
@@ -508,6 +540,43 @@ void jac_launch_tp2_local(const jacq_half_t* Q, const int32_t* BLOCK_TABLE,
                       K_SCALE_PAGES, K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES,
                       K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, 0, 1, O, nullptr, 0, stream),
            "jac_launch_tp2_local");
+}
+
+static void sparse_v1(const jacq_kivi_geometry& x, const jacq_half_t* Q,
+                      const int32_t* RETAINED_BLOCK_TABLE, const uint8_t* kc,
+                      const jacq_half_t* ks, const jacq_half_t* kz, const uint8_t* vc,
+                      const jacq_half_t* vs, const jacq_half_t* vz, const jacq_half_t* kscr,
+                      const jacq_half_t* vscr, int SEQ_LEN, int NUM_RETAINED_PAGES, float* O,
+                      hipStream_t stream, const char* where) {
+  // the kernel clamps NUM_RETAINED_PAGES to [0, dense old pages] itself
+  v1_check(run_decode(x, Q, nullptr, SEQ_LEN, RETAINED_BLOCK_TABLE, 0, kc, ks, kz, vc, vs, vz,
+                      kscr, vscr, 0, 1, O, nullptr, 0, stream,
+                      NUM_RETAINED_PAGES < 0 ? 0 : NUM_RETAINED_PAGES),
+           where);
+}
+
+void jac_launch_sparse_retained(const jacq_half_t* Q, const int32_t* RETAINED_BLOCK_TABLE,
+                                const uint8_t* K_CODE_PAGES, const jacq_half_t* K_SCALE_PAGES,
+                                const jacq_half_t* K_ZERO_PAGES, const uint8_t* V_CODE_PAGES,
+                                const jacq_half_t* V_SCALE_PAGES, const jacq_half_t* V_ZERO_PAGES,
+                                const jacq_half_t* K_RESIDUAL_SCRATCH,
+                                const jacq_half_t* V_RESIDUAL_SCRATCH, int SEQ_LEN,
+                                int NUM_RETAINED_PAGES, float* O, hipStream_t stream) {
+  sparse_v1(kGlobal, Q, RETAINED_BLOCK_TABLE, K_CODE_PAGES, K_SCALE_PAGES, K_ZERO_PAGES,
+            V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES, K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH,
+            SEQ_LEN, NUM_RETAINED_PAGES, O, stream, "jac_launch_sparse_retained");
+}
+
+void jac_launch_sparse_retained_tp2_local(
+    const jacq_half_t* Q, const int32_t* RETAINED_BLOCK_TABLE, const uint8_t* K_CODE_PAGES,
+    const jacq_half_t* K_SCALE_PAGES, const jacq_half_t* K_ZERO_PAGES,
+    const uint8_t* V_CODE_PAGES, const jacq_half_t* V_SCALE_PAGES,
+    const jacq_half_t* V_ZERO_PAGES, const jacq_half_t* K_RESIDUAL_SCRATCH,
+    const jacq_half_t* V_RESIDUAL_SCRATCH, int SEQ_LEN, int NUM_RETAINED_PAGES, float* O,
+    hipStream_t stream) {
+  sparse_v1(kTp2Local, Q, RETAINED_BLOCK_TABLE, K_CODE_PAGES, K_SCALE_PAGES, K_ZERO_PAGES,
+            V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES, K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH,
+            SEQ_LEN, NUM_RETAINED_PAGES, O, stream, "jac_launch_sparse_retained_tp2_local");
 }
 
 static void batched_v1(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t* SEQ_LENS,

@@ -47,7 +47,7 @@ __global__ __launch_bounds__(kDecThreads) void kivi_decode_simple_kernel(KiviGeo
   const int ppg = kGroup / P;
 
   int ov, rv;
-  decode_window(g, a.seq_lens ? a.seq_lens[b] : a.seq_len, &ov, &rv);
+  window_of(g, a.retained_pages, a.seq_lens ? a.seq_lens[b] : a.seq_len, &ov, &rv);
   const int n = ov + rv;
   int nsplit, chunk;
   split_plan(n, &nsplit, &chunk);
@@ -210,7 +210,7 @@ __global__ __launch_bounds__(kDecThreads) void kivi_decode_simple_kernel(KiviGeo
 __global__ __launch_bounds__(128) void kivi_combine_kernel(KiviGeo g, DecodeArgs a) {
   const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   int ov, rv;
-  decode_window(g, a.seq_lens ? a.seq_lens[b] : a.seq_len, &ov, &rv);
+  window_of(g, a.retained_pages, a.seq_lens ? a.seq_lens[b] : a.seq_len, &ov, &rv);
   int nsplit, chunk;
   split_plan(ov + rv, &nsplit, &chunk);
   if (nsplit <= 1 || d >= g.hd) return;

@@ -579,9 +579,10 @@ __device__ inline half8_t qk_softmax(WaveState<HD>& st, const SegCtx<HD>& q,
 // that an empty sequence still produces its (zero) output.
 __device__ inline int seq_tiles(const KiviGeo& g, const DecodeArgs& a, int b, int* ov, int* n) {
   int o, r;
-  decode_window(g, a.seq_lens ? ((const __attribute__((address_space(4))) int32_t*)a.seq_lens)[b]
-                              : a.seq_len,
-                &o, &r);
+  window_of(g, a.retained_pages,
+            a.seq_lens ? ((const __attribute__((address_space(4))) int32_t*)a.seq_lens)[b]
+                       : a.seq_len,
+            &o, &r);
   *ov = o;
   *n = o + r;
   return max(1, (o + r + kGroup - 1) / kGroup);

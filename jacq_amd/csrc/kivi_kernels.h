@@ -49,7 +49,26 @@ struct DecodeArgs {
   int max_splits;  // VALU kernel: split slots per (sequence, kv head)
   int batch;       // sequences (queries) in the call
   int waves;       // matrix-core kernel: wavefronts sharing the tile stream
+  int retained_pages = -1;  // >= 0: sparse-retained window (compact block table)
 };
+
+// Decode window of one sequence.  Dense: the split rule (decode_window).
+// Sparse-retained (variants.rs:2667-2680): the old tokens are the first
+// retained_pages entries of a compact table, clamped to [0, dense old pages]
+// and to the table width (whole 32-token groups when a page holds 16); the
+// residual rows keep the dense boundary, so evicted pages are skipped and are
+// never read as residual tokens.
+__host__ __device__ inline void window_of(const KiviGeo& g, int retained_pages, int seq_len,
+                                          int* old_valid, int* residual_valid) {
+  decode_window(g, seq_len, old_valid, residual_valid);
+  if (retained_pages >= 0) {
+    int pages = retained_pages;
+    const int dense_pages = *old_valid / g.page;
+    if (pages > dense_pages) pages = dense_pages;
+    if (pages > g.max_pages) pages = g.max_pages;
+    *old_valid = pages * g.page / kGroup * kGroup;
+  }
+}
 
 hipError_t launch_append(const KiviGeo& g, const AppendArgs& a, int batch, hipStream_t stream);
 // `between`, when not null, is recorded on the stream after the main kernel

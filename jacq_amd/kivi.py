@@ -94,6 +94,10 @@ def lib() -> ctypes.CDLL:
         f = getattr(L, name)
         f.argtypes = dec10 + [ctypes.c_int, _vp, _vp]
         f.restype = None
+    for name in ("jac_launch_sparse_retained", "jac_launch_sparse_retained_tp2_local"):
+        f = getattr(L, name)
+        f.argtypes = dec10 + [ctypes.c_int, ctypes.c_int, _vp, _vp]
+        f.restype = None
     for name in ("jac_launch_batched", "jac_launch_batched_tp2_local"):
         f = getattr(L, name)
         f.argtypes = [_vp] * 11 + [ctypes.c_int, _vp, _vp]
@@ -121,6 +125,10 @@ def lib() -> ctypes.CDLL:
     L.jacq_kivi_decode.argtypes = [ctypes.POINTER(Geometry)] + [_vp] * 11 + [
         _i32, _vp, _vp, ctypes.c_size_t, _vp]
     L.jacq_kivi_decode.restype = ctypes.c_int
+    L.jacq_kivi_decode_sparse_retained.argtypes = [ctypes.POINTER(Geometry), _vp, _i32, _vp,
+                                                   _i32] + [_vp] * 9 + [_vp, ctypes.c_size_t,
+                                                                        _vp]
+    L.jacq_kivi_decode_sparse_retained.restype = ctypes.c_int
     L.jacq_kivi_cache_append.argtypes = [ctypes.POINTER(Geometry)] + [_vp] * 12 + [
         _i32, _i32, _vp]
     L.jacq_kivi_cache_append.restype = ctypes.c_int
@@ -285,6 +293,45 @@ def kivi_decode_dsl(q, block_table, k_code_pages, k_scale_pages, k_zero_pages, v
     fn = lib().jac_launch_tp2_local if nh == TP2_LOCAL_NH else lib().jac_launch
     fn(_ptr(q), _ptr(block_table), *[_ptr(t) for t in pool], int(seq_len), _ptr(out),
        _stream(q.device))
+
+
+def kivi_decode_sparse_retained_dsl(q, retained_block_table, k_code_pages, k_scale_pages,
+                                    k_zero_pages, v_code_pages, v_scale_pages, v_zero_pages,
+                                    k_residual_scratch, v_residual_scratch, seq_len: int,
+                                    num_retained_pages: int, out) -> None:
+    """source_patch.py:872-971: decode over the first NUM_RETAINED_PAGES
+    entries of a compact retained-page table, residual at the dense SEQ_LEN."""
+    pool = (k_code_pages, k_scale_pages, k_zero_pages, v_code_pages, v_scale_pages, v_zero_pages,
+            k_residual_scratch, v_residual_scratch)
+    names = ("K_CODE_PAGES", "K_SCALE_PAGES", "K_ZERO_PAGES", "V_CODE_PAGES", "V_SCALE_PAGES",
+             "V_ZERO_PAGES", "K_RESIDUAL_SCRATCH", "V_RESIDUAL_SCRATCH")
+    check_cuda_tensor(q, "Q")
+    check_cuda_tensor(retained_block_table, "RETAINED_BLOCK_TABLE")
+    for t, n in zip(pool, names):
+        check_cuda_tensor(t, n)
+    check_cuda_tensor(out, "O")
+    _check_dtypes([(q, torch.float16, "Q"),
+                   (retained_block_table, torch.int32, "RETAINED_BLOCK_TABLE")]
+                  + _pool_dtypes(*pool) + [(out, torch.float32, "O")])
+    _check(k_code_pages.dim() >= 2, "K_CODE_PAGES must expose NKV at dim 1")
+    nh, nkv = q.size(0), k_code_pages.size(1)
+    real_num_blocks = k_code_pages.size(0)
+    _check_supported_geometry(nh, nkv, "kivi_decode_sparse_retained_dsl")
+    _check(real_num_blocks > 0, "K_CODE_PAGES dim 0 (page storage capacity) must be positive")
+    check_shape(q, (nh, V1_HD), "Q")
+    check_shape(retained_block_table, (OLD_BLOCKS,), "RETAINED_BLOCK_TABLE")
+    _check_pool(*pool, nkv)
+    check_shape(out, (nh, V1_HD), "O")
+    _check(1 <= seq_len <= OLD_BLOCKS * BLOCK_SIZE + RESIDUAL,
+           "SEQ_LEN must be in [1, 4096] for Qwen2.5-Coder-32B KIVI sparse-retained DSL ABI")
+    _check(0 <= num_retained_pages <= OLD_BLOCKS, "NUM_RETAINED_PAGES must be in [0, OLD_BLOCKS]")
+    _check(num_retained_pages <= real_num_blocks,
+           "NUM_RETAINED_PAGES cannot exceed physical page storage capacity")
+    check_launch_device([q, retained_block_table, *pool, out], "kivi_decode_sparse_retained_dsl")
+    fn = (lib().jac_launch_sparse_retained_tp2_local if nh == TP2_LOCAL_NH
+          else lib().jac_launch_sparse_retained)
+    fn(_ptr(q), _ptr(retained_block_table), *[_ptr(t) for t in pool], int(seq_len),
+       int(num_retained_pages), _ptr(out), _stream(q.device))
 
 
 def kivi_decode_batched_dsl(q, seq_lens, block_table, k_code_pages, k_scale_pages, k_zero_pages,
@@ -538,6 +585,31 @@ class PagedKiviCache:
         rc = lib().jacq_kivi_decode(ctypes.byref(geo), _ptr(q), _ptr(seq_lens), _ptr(block_tables),
                                     *[_ptr(t) for t in self.pool()], self.batch, _ptr(out),
                                     _ptr(workspace), ws_bytes, _stream(q.device))
+        if rc != 0:
+            raise KiviLaunchError(last_error())
+        return out
+
+    def decode_sparse_retained(self, q: torch.Tensor, seq_len: int, retained_table: torch.Tensor,
+                               num_retained_pages: int, out: torch.Tensor | None = None,
+                               workspace: torch.Tensor | None = None) -> torch.Tensor:
+        """One sequence (a batch-1 cache or sequence_view): q [NH, HD] fp16,
+        retained_table [>= num_retained_pages] int32 -> O [NH, HD] fp32."""
+        g = self.geo
+        _check(self.batch == 1, "sparse-retained decode takes one sequence (use sequence_view)")
+        check_shape(q, (g.num_heads, g.head_dim), "Q")
+        _check(q.dtype == torch.float16 and q.is_contiguous(), "Q must be contiguous fp16")
+        _check(retained_table.dtype == torch.int32 and retained_table.is_contiguous(),
+               "RETAINED_BLOCK_TABLE must be contiguous int32")
+        _check(retained_table.numel() >= num_retained_pages,
+               "RETAINED_BLOCK_TABLE holds fewer than NUM_RETAINED_PAGES entries")
+        if out is None:
+            out = torch.empty((g.num_heads, g.head_dim), dtype=torch.float32, device=q.device)
+        geo = g.c()
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        rc = lib().jacq_kivi_decode_sparse_retained(
+            ctypes.byref(geo), _ptr(q), int(seq_len), _ptr(retained_table),
+            int(num_retained_pages), *[_ptr(t) for t in self.pool()], _ptr(out),
+            _ptr(workspace), ws_bytes, _stream(q.device))
         if rc != 0:
             raise KiviLaunchError(last_error())
         return out

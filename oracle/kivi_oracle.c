@@ -381,11 +381,9 @@ static void decode_kv_head(const kivi_geo* g, int32_t h, const uint16_t* q, cons
                            const uint8_t* k_code, const uint16_t* k_scale,
                            const uint16_t* k_zero, const uint8_t* v_code,
                            const uint16_t* v_scale, const uint16_t* v_zero,
-                           const uint16_t* k_scr, const uint16_t* v_scr, int32_t seq_len,
-                           float* out) {
+                           const uint16_t* k_scr, const uint16_t* v_scr, int32_t ov,
+                           int32_t rv, float* out) {
   const int32_t HD = g->hd, G = g->nh / g->nkv;
-  int32_t ov, rv;
-  decode_window(g, seq_len, &ov, &rv);
   float* qf = (float*)malloc(sizeof(float) * (size_t)g->nh * HD);
   float* m = (float*)malloc(sizeof(float) * (size_t)G);
   float* l = (float*)malloc(sizeof(float) * (size_t)G);
@@ -417,20 +415,20 @@ void kivi_ref_decode_online(const kivi_geo* g, const uint16_t* q, const int32_t*
                             const uint16_t* v_scale, const uint16_t* v_zero,
                             const uint16_t* k_scr, const uint16_t* v_scr, int32_t seq_len,
                             float* out) {
-  for (int32_t h = 0; h < g->nkv; ++h)
-    decode_kv_head(g, h, q, block_table, k_code, k_scale, k_zero, v_code, v_scale, v_zero,
-                   k_scr, v_scr, seq_len, out);
-}
-
-void kivi_ref_decode_twopass(const kivi_geo* g, const uint16_t* q, const int32_t* block_table,
-                             const uint8_t* k_code, const uint16_t* k_scale,
-                             const uint16_t* k_zero, const uint8_t* v_code,
-                             const uint16_t* v_scale, const uint16_t* v_zero,
-                             const uint16_t* k_scr, const uint16_t* v_scr, int32_t seq_len,
-                             double* out) {
-  const int32_t HD = g->hd, G = g->nh / g->nkv;
   int32_t ov, rv;
   decode_window(g, seq_len, &ov, &rv);
+  for (int32_t h = 0; h < g->nkv; ++h)
+    decode_kv_head(g, h, q, block_table, k_code, k_scale, k_zero, v_code, v_scale, v_zero,
+                   k_scr, v_scr, ov, rv, out);
+}
+
+static void twopass_window(const kivi_geo* g, const uint16_t* q, const int32_t* block_table,
+                           const uint8_t* k_code, const uint16_t* k_scale,
+                           const uint16_t* k_zero, const uint8_t* v_code,
+                           const uint16_t* v_scale, const uint16_t* v_zero,
+                           const uint16_t* k_scr, const uint16_t* v_scr, int32_t ov, int32_t rv,
+                           double* out) {
+  const int32_t HD = g->hd, G = g->nh / g->nkv;
   const int32_t n = ov + rv;
   float* k = (float*)malloc(sizeof(float) * (size_t)HD);
   float* v = (float*)malloc(sizeof(float) * (size_t)HD);
@@ -497,6 +495,64 @@ void kivi_ref_decode_twopass(const kivi_geo* g, const uint16_t* q, const int32_t
   free(sc);
 }
 
+void kivi_ref_decode_twopass(const kivi_geo* g, const uint16_t* q, const int32_t* block_table,
+                             const uint8_t* k_code, const uint16_t* k_scale,
+                             const uint16_t* k_zero, const uint8_t* v_code,
+                             const uint16_t* v_scale, const uint16_t* v_zero,
+                             const uint16_t* k_scr, const uint16_t* v_scr, int32_t seq_len,
+                             double* out) {
+  int32_t ov, rv;
+  decode_window(g, seq_len, &ov, &rv);
+  twopass_window(g, q, block_table, k_code, k_scale, k_zero, v_code, v_scale, v_zero, k_scr,
+                 v_scr, ov, rv, out);
+}
+
+/* ---- sparse-retained decode, variants.rs:2620-2740 ---- */
+
+/* Window of variants.rs:2667-2680: the old tokens are the first
+ * num_retained_pages entries of the compact table, clamped to [0, dense old
+ * pages] and to the table width (whole groups at page 16); the residual rows
+ * keep the dense SEQ_LEN boundary, so evicted pages are skipped and never read
+ * as residual tokens. */
+static void sparse_window(const kivi_geo* g, int32_t seq_len, int32_t num_retained_pages,
+                          int32_t* old_valid, int32_t* residual_valid) {
+  int32_t dense_ov;
+  decode_window(g, seq_len, &dense_ov, residual_valid);
+  int32_t pages = num_retained_pages < 0 ? 0 : num_retained_pages;
+  const int32_t dense_pages = dense_ov / g->page;
+  if (pages > dense_pages) pages = dense_pages;
+  if (pages > g->max_pages) pages = g->max_pages;
+  *old_valid = (pages * g->page / g->group) * g->group;
+}
+
+void kivi_ref_decode_sparse_retained(const kivi_geo* g, const uint16_t* q,
+                                     const int32_t* retained_table, const uint8_t* k_code,
+                                     const uint16_t* k_scale, const uint16_t* k_zero,
+                                     const uint8_t* v_code, const uint16_t* v_scale,
+                                     const uint16_t* v_zero, const uint16_t* k_scr,
+                                     const uint16_t* v_scr, int32_t seq_len,
+                                     int32_t num_retained_pages, float* out) {
+  int32_t ov, rv;
+  sparse_window(g, seq_len, num_retained_pages, &ov, &rv);
+  for (int32_t h = 0; h < g->nkv; ++h)
+    decode_kv_head(g, h, q, retained_table, k_code, k_scale, k_zero, v_code, v_scale, v_zero,
+                   k_scr, v_scr, ov, rv, out);
+}
+
+void kivi_ref_decode_sparse_retained_twopass(const kivi_geo* g, const uint16_t* q,
+                                             const int32_t* retained_table,
+                                             const uint8_t* k_code, const uint16_t* k_scale,
+                                             const uint16_t* k_zero, const uint8_t* v_code,
+                                             const uint16_t* v_scale, const uint16_t* v_zero,
+                                             const uint16_t* k_scr, const uint16_t* v_scr,
+                                             int32_t seq_len, int32_t num_retained_pages,
+                                             double* out) {
+  int32_t ov, rv;
+  sparse_window(g, seq_len, num_retained_pages, &ov, &rv);
+  twopass_window(g, q, retained_table, k_code, k_scale, k_zero, v_code, v_scale, v_zero, k_scr,
+                 v_scr, ov, rv, out);
+}
+
 void kivi_ref_decode_batch(const kivi_geo* g, const uint16_t* q, const int32_t* seq_lens,
                            const int32_t* block_tables, const uint8_t* k_code,
                            const uint16_t* k_scale, const uint16_t* k_zero,
@@ -514,9 +570,11 @@ void kivi_ref_decode_batch(const kivi_geo* g, const uint16_t* q, const int32_t* 
 #endif
   for (int32_t w = 0; w < work; ++w) {
     const int32_t b = w / g->nkv, h = w % g->nkv;
+    int32_t ov, rv;
+    decode_window(g, seq_lens[b], &ov, &rv);
     decode_kv_head(g, h, q + b * qo_seq, block_tables + (int64_t)b * g->max_pages, k_code,
                    k_scale, k_zero, v_code, v_scale, v_zero, k_scr + b * scr_seq,
-                   v_scr + b * scr_seq, seq_lens[b], out + b * qo_seq);
+                   v_scr + b * scr_seq, ov, rv, out + b * qo_seq);
   }
 }
 

@@ -109,6 +109,27 @@ void kivi_ref_decode_twopass(const kivi_geo* g, const uint16_t* q, const int32_t
                              const uint16_t* k_scr, const uint16_t* v_scr, int32_t seq_len,
                              double* out);
 
+/* Sparse-retained decode (variants.rs:2620-2740): old tokens from the first
+ * num_retained_pages entries of the compact retained_table (clamped to the
+ * dense old pages and the table width), residual rows at the dense SEQ_LEN
+ * boundary. */
+void kivi_ref_decode_sparse_retained(const kivi_geo* g, const uint16_t* q,
+                                     const int32_t* retained_table, const uint8_t* k_code,
+                                     const uint16_t* k_scale, const uint16_t* k_zero,
+                                     const uint8_t* v_code, const uint16_t* v_scale,
+                                     const uint16_t* v_zero, const uint16_t* k_scr,
+                                     const uint16_t* v_scr, int32_t seq_len,
+                                     int32_t num_retained_pages, float* out);
+/* The same window through the float64 two-pass attention. */
+void kivi_ref_decode_sparse_retained_twopass(const kivi_geo* g, const uint16_t* q,
+                                             const int32_t* retained_table,
+                                             const uint8_t* k_code, const uint16_t* k_scale,
+                                             const uint16_t* k_zero, const uint8_t* v_code,
+                                             const uint16_t* v_scale, const uint16_t* v_zero,
+                                             const uint16_t* k_scr, const uint16_t* v_scr,
+                                             int32_t seq_len, int32_t num_retained_pages,
+                                             double* out);
+
 /* Batch driver for the CPU baseline: q [B,NH,HD], seq_lens [B], block_tables
  * [B,max_pages], scratch [B,NKV,R+group,HD], out [B,NH,HD].  Runs
  * kivi_ref_decode_online per (sequence, kv head) with the G query heads of a

@@ -214,6 +214,21 @@ def decode_twopass(cache: Cache, b: int, q: np.ndarray, block_table: np.ndarray,
     return out
 
 
+def decode_sparse_retained(cache: Cache, b: int, q: np.ndarray, retained_table: np.ndarray,
+                           seq_len: int, num_retained_pages: int,
+                           twopass: bool = False) -> np.ndarray:
+    """Sparse-retained decode (kivi_oracle.c, variants.rs:2620-2740): fp32
+    online softmax, or the float64 two-pass attention with twopass."""
+    g = cache.geo
+    out = np.zeros((g.nh, g.hd), np.float64 if twopass else np.float32)
+    fn = (lib().kivi_ref_decode_sparse_retained_twopass if twopass
+          else lib().kivi_ref_decode_sparse_retained)
+    fn(ctypes.byref(g.c()), _p(np.ascontiguousarray(q)),
+       _p(np.ascontiguousarray(retained_table, np.int32)), *cache.pool_args(), *cache.scr(b),
+       seq_len, num_retained_pages, _p(out))
+    return out
+
+
 def decode_splitk(cache: Cache, b: int, q: np.ndarray, block_table: np.ndarray,
                   seq_len: int, chunk: int) -> np.ndarray:
     g = cache.geo

@@ -32,15 +32,26 @@ def decode_window(seq_len: int, residual: int, lq: int) -> tuple[int, int]:
     return old, res
 
 
+def sparse_window(seq_len: int, residual: int, lq: int, page: int, max_pages: int,
+                  retained: int) -> tuple[int, int]:
+    """variants.rs:2667-2680: old tokens = the retained pages (clamped to
+    [0, dense old pages] and the table width, whole groups), residual rows at
+    the dense boundary."""
+    dense_old, res = decode_window(seq_len, residual, lq)
+    pages = min(max(retained, 0), dense_old // page, max_pages)
+    return pages * page // GROUP * GROUP, res
+
+
 def dequant_sequence(cache, b: int, block_table: np.ndarray, seq_len: int,
-                     value_parts: bool = False):
-    """K, V [NKV, n, HD] float64 of the decode window of sequence b; with
-    value_parts, V is returned as (code * scale, zero) of the quantised tokens
-    (residual tokens: (value, 0))."""
+                     value_parts: bool = False, window: tuple[int, int] | None = None):
+    """K, V [NKV, n, HD] float64 of the decode window of sequence b (or of an
+    explicit (old, residual) window over block_table); with value_parts, V is
+    returned as (code * scale, zero) of the quantised tokens (residual tokens:
+    (value, 0))."""
     g = cache.geo
     page, hd, nkv = g.page, g.hd, g.nkv
     lq = (g.max_pages * page) // GROUP * GROUP
-    old, res = decode_window(seq_len, g.residual, lq)
+    old, res = window if window is not None else decode_window(seq_len, g.residual, lq)
     n = old + res
     K = np.zeros((nkv, n, hd))
     V = np.zeros((nkv, n, hd))

@@ -66,13 +66,15 @@ def test_header_declares_the_reference_symbols():
     for name in ("jac_launch", "jac_launch_tp2_local", "jac_launch_batched",
                  "jac_launch_batched_tp2_local", "jac_launch_cache_write",
                  "jac_launch_cache_write_batched", "kivi_cache_write_launch",
-                 "kivi_cache_write_batched_launch"):
+                 "kivi_cache_write_batched_launch", "jac_launch_sparse_retained",
+                 "jac_launch_sparse_retained_tp2_local"):
         assert name in fns, name
     ext = sorted(n for n in fns if n.startswith("jacq_kivi_"))
     assert ext == sorted([
         "jacq_kivi_abi_version", "jacq_kivi_ext_version", "jacq_kivi_last_error",
         "jacq_kivi_check_geometry", "jacq_kivi_max_seq_len", "jacq_kivi_check_block_table_width",
         "jacq_kivi_decode_workspace_size", "jacq_kivi_decode", "jacq_kivi_cache_append",
+        "jacq_kivi_decode_sparse_retained",
         "jacq_kivi_plan_batched_write", "jacq_kivi_profile_start", "jacq_kivi_profile_stop",
         "jacq_kivi_profile_write_ms"])
 
@@ -90,6 +92,12 @@ def test_jac_launch_argument_order_matches_reference():
     order = list(bindings.JAC_LAUNCH_ORDER)
     assert order[:-1] == params[:-1] and order[-1].endswith("stream")
     assert "K_RESIDUAL" not in order and "V_RESIDUAL" not in order
+    # source_patch.py:589-595: the dense order with RETAINED_BLOCK_TABLE and
+    # NUM_RETAINED_PAGES in place of BLOCK_TABLE and after SEQ_LEN
+    sparse = header_functions()["jac_launch_sparse_retained"]
+    assert sparse == (["Q", "RETAINED_BLOCK_TABLE"] + params[2:11] + ["NUM_RETAINED_PAGES", "O",
+                                                                      "stream"])
+    assert header_functions()["jac_launch_sparse_retained_tp2_local"] == sparse
     batched = header_functions()["jac_launch_batched"]
     assert batched[:3] == ["Q", "SEQ_LENS", "BLOCK_TABLE"] and batched[-3:] == [
         "NUM_QUERIES", "O", "stream"]
@@ -246,6 +254,11 @@ extern "C" void jac_launch(const __half* Q, const int* BLOCK_TABLE,
     const unsigned char* V_CODE_PAGES, const __half* V_SCALE_PAGES, const __half* V_ZERO_PAGES,
     const __half* K_RESIDUAL_SCRATCH, const __half* V_RESIDUAL_SCRATCH,
     int SEQ_LEN, float* O, hipStream_t stream);
+extern "C" void jac_launch_sparse_retained(const __half* Q, const int* RETAINED_BLOCK_TABLE,
+    const unsigned char* K_CODE_PAGES, const __half* K_SCALE_PAGES, const __half* K_ZERO_PAGES,
+    const unsigned char* V_CODE_PAGES, const __half* V_SCALE_PAGES, const __half* V_ZERO_PAGES,
+    const __half* K_RESIDUAL_SCRATCH, const __half* V_RESIDUAL_SCRATCH,
+    int SEQ_LEN, int NUM_RETAINED_PAGES, float* O, hipStream_t stream);
 void kivi_cache_write_launch(unsigned char* K_CODE_PAGES, __half* K_SCALE_PAGES,
     __half* K_ZERO_PAGES, unsigned char* V_CODE_PAGES, __half* V_SCALE_PAGES,
     __half* V_ZERO_PAGES, __half* K_RESIDUAL_SCRATCH, __half* V_RESIDUAL_SCRATCH,
@@ -260,6 +273,8 @@ int main(int argc, char**) {
   if (argc > 99) {  // referenced, never called: no GPU work on the CPU
     jac_launch(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                nullptr, 0, nullptr, nullptr);
+    jac_launch_sparse_retained(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                               nullptr, nullptr, nullptr, 0, 0, nullptr, nullptr);
     kivi_cache_write_launch(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                             nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, nullptr);
     kivi_cache_write_batched_launch(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
@@ -289,3 +304,25 @@ def test_runtime_entry_points_reject_unaligned_pointers(native):
     append[8] = odd  # NEW_K
     assert native.jacq_kivi_cache_append(ctypes.byref(g), *append, 1, 1, None) == 1
     assert b"16-byte aligned" in native.jacq_kivi_last_error()
+
+
+def test_sparse_retained_entry_point_rejects_like_reference(native):
+    """The runtime sparse-retained entry point applies the reference op's
+    NUM_RETAINED_PAGES / SEQ_LEN checks (source_patch.py:942-945) before any
+    HIP call."""
+    g = geo()  # 124-entry table, 1000 pages
+    ok = 1 << 20
+    caches = [ok] * 8
+
+    def call(seq_len, retained):
+        return native.jacq_kivi_decode_sparse_retained(ctypes.byref(g), ok, seq_len, ok,
+                                                       retained, *caches, ok, None, 0, None)
+    for seq_len, retained, msg in ((4096, -1, b"NUM_RETAINED_PAGES"),
+                                   (4096, 125, b"NUM_RETAINED_PAGES"),
+                                   (0, 3, b"SEQ_LEN"), (124 * 32 + 129, 3, b"SEQ_LEN")):
+        assert call(seq_len, retained) == 1
+        assert msg in native.jacq_kivi_last_error()
+    small = geo(num_pages=10)
+    assert native.jacq_kivi_decode_sparse_retained(ctypes.byref(small), ok, 4096, ok, 11,
+                                                   *caches, ok, None, 0, None) == 1
+    assert b"physical page storage" in native.jacq_kivi_last_error()

@@ -8,7 +8,11 @@ are checked against
   * uniform keys -> the plain mean of the dequantised values;
   * seq_len <= residual -> ordinary fp16 attention on the raw history;
   * physical-page permutation invariance, split-K == one pass, the LSE merge
-    closed form, empty and over-long sequences.
+    closed form, empty and over-long sequences;
+  * sparse-retained decode (variants.rs:2620-2740): full retention == dense,
+    no retention == residual-only attention, a retained subset == numpy
+    attention over exactly those tokens plus the dense residual window, and
+    the clamps of NUM_RETAINED_PAGES.
 """
 from __future__ import annotations
 
@@ -134,3 +138,68 @@ def test_workload_generator_is_deterministic():
     w = wl.WORKLOADS["qwen05b"]
     r1, r2 = np.random.default_rng(w.seed), np.random.default_rng(w.seed)
     assert np.array_equal(wl.context_lens(w, r1), wl.context_lens(w, r2))
+
+
+# ---------------------------------------------------------------- sparse-retained
+
+def _sparse_case(n=400, seed=31):
+    c, q, table, _, _ = build(GEO, n, seed=seed)
+    lq = (GEO.max_pages * GEO.page) // 32 * 32
+    dense_old, res = nref.decode_window(n, GEO.residual, lq)
+    return c, q, table, dense_old, res
+
+
+def test_sparse_full_retention_equals_dense():
+    n = 400
+    c, q, table, dense_old, _ = _sparse_case(n)
+    pages = dense_old // GEO.page
+    compact = np.ascontiguousarray(table[:pages])
+    np.testing.assert_array_equal(o.decode_sparse_retained(c, 0, q, compact, n, pages),
+                                  o.decode_online(c, 0, q, table, n))
+    np.testing.assert_array_equal(o.decode_sparse_retained(c, 0, q, compact, n, pages, True),
+                                  o.decode_twopass(c, 0, q, table, n))
+
+
+def test_sparse_zero_retention_is_residual_attention():
+    n = 400
+    c, q, table, dense_old, res = _sparse_case(n)
+    K, V = nref.dequant_sequence(c, 0, table, n, window=(0, res))
+    want = nref.attention(q, K, V)
+    # the scratch rows are the tokens after the dense boundary
+    assert K.shape[1] == n - dense_old
+    np.testing.assert_allclose(o.decode_sparse_retained(c, 0, q, table[:0], n, 0, True), want,
+                               rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("groups", [[0], [3, 5, 9], [9, 0, 4, 2], list(range(10))])
+def test_sparse_subset_matches_numpy(groups):
+    """Retained groups in any order (a compact table of their pages): numpy
+    attention over exactly those tokens, then the dense residual rows."""
+    n = 400
+    c, q, table, dense_old, res = _sparse_case(n)
+    per = 32 // GEO.page
+    compact = np.concatenate([table[g * per:(g + 1) * per] for g in groups]).astype(np.int32)
+    npages = len(compact)
+    K, V = nref.dequant_sequence(c, 0, compact, n, window=(npages * GEO.page, res))
+    want = nref.attention(q, K, V)
+    np.testing.assert_allclose(o.decode_sparse_retained(c, 0, q, compact, n, npages, True), want,
+                               rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(o.decode_sparse_retained(c, 0, q, compact, n, npages), want,
+                               rtol=1e-4, atol=2e-5)
+
+
+def test_sparse_clamps_retained_pages():
+    n = 400
+    c, q, table, dense_old, _ = _sparse_case(n)
+    pages = dense_old // GEO.page
+    full = o.decode_sparse_retained(c, 0, q, table, n, pages)
+    # more pages than the dense window holds -> the dense window
+    np.testing.assert_array_equal(o.decode_sparse_retained(c, 0, q, table, n, pages + 3), full)
+    # negative -> none retained
+    np.testing.assert_array_equal(o.decode_sparse_retained(c, 0, q, table, n, -2),
+                                  o.decode_sparse_retained(c, 0, q, table, n, 0))
+    # page 16: an odd count covers whole groups only
+    np.testing.assert_array_equal(o.decode_sparse_retained(c, 0, q, table, n, 5),
+                                  o.decode_sparse_retained(c, 0, q, table, n, 4))
+    lq = (GEO.max_pages * GEO.page) // 32 * 32
+    assert nref.sparse_window(n, GEO.residual, lq, GEO.page, GEO.max_pages, 5) == (64, n - dense_old)
