@@ -296,10 +296,12 @@ int32_t jacq_kivi_plan_batched_write(int32_t start_seq_len, int32_t num_new, int
  * events on its own stream around its kernels.  jacq_kivi_profile_stop
  * disables recording, waits for the events and writes the per-call
  * milliseconds of the decode main kernel and of its split-K merge (at most
- * cap entries); it returns the number of decode calls written or -1.
- * jacq_kivi_profile_write_ms then writes the per-call milliseconds of the
- * cache-write kernel recorded in the same window. */
-int jacq_kivi_profile_start(int32_t max_calls);
+ * cap entries); it returns the number of decode calls written or -1.  With
+ * split == 0 no event is recorded between the two decode launches (the
+ * marker costs a few microseconds): kernel_ms then holds the whole decode and
+ * merge_ms zero.  jacq_kivi_profile_write_ms then writes the per-call
+ * milliseconds of the cache-write kernel recorded in the same window. */
+int jacq_kivi_profile_start(int32_t max_calls, int32_t split);
 int32_t jacq_kivi_profile_stop(float* kernel_ms, float* merge_ms, int32_t cap);
 int32_t jacq_kivi_profile_write_ms(float* ms, int32_t cap);
 

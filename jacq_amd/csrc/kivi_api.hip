@@ -175,9 +175,11 @@ void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& 
 // ---- measurement hook: HIP events around the two decode launches ----
 // While enabled, each decode call takes the next triple of a pre-created
 // event pool and records it on the call's own stream: before the main
-// kernel, between it and the split-K merge, and after the merge.
+// kernel, between it and the split-K merge (split mode only: the marker
+// itself costs a few microseconds), and after the merge.
 struct Profiler {
   bool on = false;
+  bool split = true;
   int used = 0, wused = 0;
   std::vector<hipEvent_t> ev;   // decode: 3 per call
   std::vector<hipEvent_t> wev;  // cache write: 2 per call
@@ -189,6 +191,7 @@ void profile_slot(hipEvent_t out[3]) {
   std::lock_guard<std::mutex> lk(g_prof_mu);
   if (!g_prof.on || 3 * (g_prof.used + 1) > (int)g_prof.ev.size()) return;
   for (int i = 0; i < 3; ++i) out[i] = g_prof.ev[3 * g_prof.used + i];
+  if (!g_prof.split) out[1] = nullptr;
   ++g_prof.used;
 }
 
@@ -434,7 +437,7 @@ int jacq_kivi_cache_append(const jacq_kivi_geometry* geo, uint8_t* K_CODE_PAGES,
 }
 
 // plan_batched_write, source_patch.py:504-553.
-int jacq_kivi_profile_start(int32_t max_calls) {
+int jacq_kivi_profile_start(int32_t max_calls, int32_t split) {
   if (max_calls < 1) return fail(JACQ_KIVI_EINVAL, "max_calls must be >= 1");
   std::lock_guard<std::mutex> lk(g_prof_mu);
   for (auto* pool : {&g_prof.ev, &g_prof.wev}) {
@@ -447,6 +450,7 @@ int jacq_kivi_profile_start(int32_t max_calls) {
   }
   g_prof.used = 0;
   g_prof.wused = 0;
+  g_prof.split = split != 0;
   g_prof.on = true;
   return JACQ_KIVI_OK;
 }
@@ -457,8 +461,15 @@ int32_t jacq_kivi_profile_stop(float* kernel_ms, float* merge_ms, int32_t cap) {
   const int n = g_prof.used < cap ? g_prof.used : cap;
   for (int i = 0; i < n; ++i) {
     hipEvent_t* e = &g_prof.ev[3 * i];
-    if (hipEventSynchronize(e[2]) != hipSuccess ||
-        hipEventElapsedTime(&kernel_ms[i], e[0], e[1]) != hipSuccess ||
+    if (hipEventSynchronize(e[2]) != hipSuccess)
+      return fail(JACQ_KIVI_EHIP, "event timing failed");
+    if (!g_prof.split) {  // the whole decode in kernel_ms
+      merge_ms[i] = 0.0f;
+      if (hipEventElapsedTime(&kernel_ms[i], e[0], e[2]) != hipSuccess)
+        return fail(JACQ_KIVI_EHIP, "event timing failed");
+      continue;
+    }
+    if (hipEventElapsedTime(&kernel_ms[i], e[0], e[1]) != hipSuccess ||
         hipEventElapsedTime(&merge_ms[i], e[1], e[2]) != hipSuccess)
       return fail(JACQ_KIVI_EHIP, "event timing failed");
   }

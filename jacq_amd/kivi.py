@@ -135,7 +135,7 @@ def lib() -> ctypes.CDLL:
     L.jacq_kivi_plan_batched_write.argtypes = [_i32, _i32, _i32, _i32, ctypes.POINTER(Subchunk),
                                                _i32]
     L.jacq_kivi_plan_batched_write.restype = _i32
-    L.jacq_kivi_profile_start.argtypes = [_i32]
+    L.jacq_kivi_profile_start.argtypes = [_i32, _i32]
     L.jacq_kivi_profile_start.restype = ctypes.c_int
     L.jacq_kivi_profile_stop.argtypes = [ctypes.POINTER(ctypes.c_float),
                                          ctypes.POINTER(ctypes.c_float), _i32]
@@ -150,9 +150,10 @@ def last_error() -> str:
     return lib().jacq_kivi_last_error().decode()
 
 
-def profile_start(max_calls: int) -> None:
-    """Record HIP events around the next max_calls decode calls."""
-    if lib().jacq_kivi_profile_start(max_calls) != 0:
+def profile_start(max_calls: int, split: bool = True) -> None:
+    """Record HIP events around the next max_calls decode calls; with split,
+    also between the main kernel and the merge."""
+    if lib().jacq_kivi_profile_start(max_calls, int(split)) != 0:
         raise KiviLaunchError(last_error())
 
 
