@@ -588,6 +588,25 @@ __device__ inline int seq_tiles(const KiviGeo& g, const DecodeArgs& a, int b, in
   return max(1, (o + r + kGroup - 1) / kGroup);
 }
 
+// Work units of the stream-K split.  An fp16 residual tile moves 16 KiB per
+// kv head at HD=128 with its load latency exposed, a quantised group 5 KiB
+// from the LDS ring, so a residual tile weighs kResidualUnits: the split then
+// gives every wavefront about the same bytes (by tile count, the waves that
+// end a sequence finished last).
+constexpr int kResidualUnits = 3;
+__device__ inline int seq_units(const KiviGeo& g, const DecodeArgs& a, int b) {
+  int ov, n;
+  const int T = seq_tiles(g, a, b, &ov, &n);
+  const int nq = ov / kGroup;
+  return nq + kResidualUnits * (T - nq);
+}
+// First tile of a segment (nq quantised groups, then residual tiles) whose
+// first unit is at or after unit u: the tiles owned by a unit range [u0, u1)
+// are [tile_at(u0), tile_at(u1)).
+__device__ inline int tile_at(int u, int nq) {
+  return u <= nq ? u : nq + (u - nq + kResidualUnits - 1) / kResidualUnits;
+}
+
 __device__ inline int wave_sum_i(int v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -604,30 +623,30 @@ __device__ inline int wave_incl_scan(int v, int lane) {
 }
 
 // Total tiles of the concatenated streams (all sequences x kv heads).
-__device__ inline int64_t stream_tiles(const KiviGeo& g, const DecodeArgs& a, int lane) {
+__device__ inline int64_t stream_units(const KiviGeo& g, const DecodeArgs& a, int lane) {
   int64_t tot = 0;
   for (int base = 0; base < a.batch; base += 64) {
-    int T = 0, ov, n;
-    if (base + lane < a.batch) T = seq_tiles(g, a, base + lane, &ov, &n);
-    tot += __builtin_amdgcn_readfirstlane(wave_sum_i(T));
+    int U = 0;
+    if (base + lane < a.batch) U = seq_units(g, a, base + lane);
+    tot += __builtin_amdgcn_readfirstlane(wave_sum_i(U));
   }
   return tot * g.nkv;
 }
 
 // Wavefronts that share the stream: at most gridDim.x, and at least
-// kMinTilesPerWave tiles each so that tiny batches do not scatter.
-constexpr int kMinTilesPerWave = 8;
-__device__ inline int64_t stream_waves(int64_t tiles, int grid) {
-  int64_t w = (tiles + kMinTilesPerWave - 1) / kMinTilesPerWave;
+// kMinUnitsPerWave units each so that tiny batches do not scatter.
+constexpr int kMinUnitsPerWave = 8;
+__device__ inline int64_t stream_waves(int64_t units, int grid) {
+  int64_t w = (units + kMinUnitsPerWave - 1) / kMinUnitsPerWave;
   if (w < 1) w = 1;
   return w < grid ? w : grid;
 }
 
-// Start of a sequence's stream (in tiles, times NKV) and its tile count.
+// Start of a sequence's stream (in units, times NKV) and its unit count.
 struct SeqSpan {
   int b;
-  int64_t start;  // global tile index of (b, kv head 0)
-  int tiles;      // tiles per kv head
+  int64_t start;  // global unit index of (b, kv head 0)
+  int units;      // units per kv head
 };
 
 // The sequence whose streams contain global tile x.
@@ -635,8 +654,8 @@ __device__ inline SeqSpan locate(const KiviGeo& g, const DecodeArgs& a, int64_t 
   int64_t run = 0;
   for (int base = 0; base < a.batch; base += 64) {
     const int bb = base + lane;
-    int T = 0, ov, n;
-    if (bb < a.batch) T = seq_tiles(g, a, bb, &ov, &n);
+    int T = 0;
+    if (bb < a.batch) T = seq_units(g, a, bb);
     const int incl = wave_incl_scan(T, lane);
     const uint64_t hit = __builtin_amdgcn_ballot_w64(bb < a.batch && run + (int64_t)g.nkv * incl > x);
     if (hit) {
@@ -697,7 +716,7 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
 
   const int lane = threadIdx.x, c = lane & 15, j = lane >> 4;
   const int G = g.gqa, NKV = g.nkv;
-  const int64_t TT = stream_tiles(g, a, lane);
+  const int64_t TT = stream_units(g, a, lane);
   const int64_t W = stream_waves(TT, gridDim.x);
   const int w = blockIdx.x;
   if (w >= W) return;
@@ -721,27 +740,43 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
   // priority at every quarter of its own run, so a wave behind its partner
   // outranks it and the pair ends closer together.
   const int n_run = (int)(x1 - x0), q1 = n_run / 4, q2 = n_run / 2, q3 = 3 * n_run / 4;
-  int done = 0;
+  int done = 0, level = 3;
   __builtin_amdgcn_s_setprio(3);
-  auto progress = [&]() {
-    ++done;
-    if (done == q1)
+  auto progress = [&](int units) {
+    done += units;
+    if (level == 3 && done >= q1) {
       __builtin_amdgcn_s_setprio(2);
-    else if (done == q2)
+      level = 2;
+    }
+    if (level == 2 && done >= q2) {
       __builtin_amdgcn_s_setprio(1);
-    else if (done == q3)
+      level = 1;
+    }
+    if (level == 1 && done >= q3) {
       __builtin_amdgcn_s_setprio(0);
+      level = 0;
+    }
   };
   SeqSpan sp = locate(g, a, x0, lane);
-  int kvh = (int)((x0 - sp.start) / sp.tiles);
-  int t = (int)((x0 - sp.start) % sp.tiles);
+  int kvh = (int)((x0 - sp.start) / sp.units);
+  int u = (int)((x0 - sp.start) % sp.units);  // unit offset inside the segment
   int64_t x = x0;
   while (x < x1) {
     const int b = sp.b, h = kvh;
     int ov, n;
     const int T = seq_tiles(g, a, b, &ov, &n);
-    const int t_beg = t;
-    const int t_fin = (int)min((int64_t)T, t + (x1 - x));
+    const int nq = ov / kGroup;
+    const int u_end = (int)min((int64_t)(nq + kResidualUnits * (T - nq)), u + (x1 - x));
+    const int t_beg = tile_at(u, nq), t_fin = tile_at(u_end, nq);
+    x += u_end - u;
+    u = 0;
+    if (++kvh == NKV) {
+      kvh = 0;
+      sp.b += 1;
+    }
+    // the run starts inside this segment's last residual tile, which the
+    // previous wavefront owns: nothing here (no partial, no map entry)
+    if (t_beg >= t_fin) continue;
 
     // ---- quantised groups: a ring of S LDS stages, S - 1 in flight ----
     const int tq_end = min(t_fin, ov / kGroup);
@@ -807,7 +842,7 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
         st.ob = mfma(pa, as_h8(vd.vz4), st.ob);  // sum_t P z_t
         pv_group<HD>(st, pa, vd, nb, big_scales(vd));
         slot = slot == S - 1 ? 0 : slot + 1;
-        progress();
+        progress(1);
       }
     }
 
@@ -844,7 +879,7 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
       // Sigma P into the sum columns (the fp16 tokens carry no zero point)
       const uint32_t one2 = sum_col ? 0x3C003C00u : 0u;
       st.ob = mfma(pr, as_h8(u32x4{one2, one2, one2, one2}), st.ob);
-      progress();
+      progress(kResidualUnits);
     }
 
     // ---- segment output: O directly, or a partial for the combine kernel ----
@@ -887,13 +922,6 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
       const int64_t seg = (int64_t)b * NKV + h;
       if (t_beg == 0) a.ws_seg[2 * seg] = w;
       if (t_fin == T) a.ws_seg[2 * seg + 1] = w;
-    }
-
-    x += t_fin - t_beg;
-    t = 0;
-    if (++kvh == NKV) {
-      kvh = 0;
-      sp.b += 1;
     }
   }
 }
