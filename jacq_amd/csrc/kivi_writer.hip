@@ -89,6 +89,49 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
     return nv + (int64_t)(p - r0) * tok_stride;
   };
 
+  // The first aged group's 32 rows go to LDS (the stores below cannot touch
+  // them: phase 1 writes rows >= r0, the shift only after its barrier).  All
+  // of a thread's loads are issued before its LDS stores: one memory latency.
+  constexpr int kTilePer = kGroup * 128 / 8 / kWriterThreads;  // w4 per thread, HD <= 128
+  w4 tk[kTilePer], tv[kTilePer];
+  auto load_tile = [&](int gi) {
+#pragma unroll
+    for (int j = 0; j < kTilePer; ++j) {
+      const int i = min(tid + j * kWriterThreads, kGroup * VPR - 1);
+      const int t = i / VPR, c = i % VPR;
+      tk[j] = *(const w4*)(krow(gi * kGroup + t) + c * 8);
+      tv[j] = *(const w4*)(vrow(gi * kGroup + t) + c * 8);
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int j = 0; j < kTilePer; ++j) {
+      const int i = tid + j * kWriterThreads;
+      if (i < kGroup * VPR) {
+        k_tile[i] = tk[j];
+        v_tile[i] = tv[j];
+      }
+    }
+  };
+  // Physical pages of an aged group (first_page, first_page + 1 at page 16),
+  // read through the constant address space: wave-uniform scalar loads,
+  // issued for the first group together with its tile.
+  const __attribute__((address_space(4))) int32_t* btc =
+      (const __attribute__((address_space(4))) int32_t*)bt;
+  auto group_pages = [&](int gi, int* p0, int* p1) {
+    const int fp = (old0 / kGroup + gi) * ppg;
+    *p0 = *p1 = -1;
+    if (fp + ppg <= g.max_pages) {
+      *p0 = btc[fp];
+      if (ppg == 2) *p1 = btc[fp + 1];
+    }
+  };
+  int gp0 = -1, gp1 = -1;
+  if (D > 0) {
+    group_pages(0, &gp0, &gp1);
+    load_tile(0);
+  }
+
   // Shift sources of the first pass (phase 3), loaded now so that their
   // latency overlaps the quantisation.
   constexpr int kShiftRows = 128;
@@ -96,26 +139,20 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
   const bool shift = !(in_scratch && D == 0);
   w4 shk[kPer], shv[kPer];
   const int rows0 = shift ? min(kShiftRows, r1) : 0;
+  // every load unconditional (a lane past the last row re-reads the last
+  // row): under a per-lane branch the compiler waited for each load before
+  // issuing the next
+  if (rows0 > 0) {
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int i = tid + j * kWriterThreads;
-    if (i < rows0 * VPR) {
+    for (int j = 0; j < kPer; ++j) {
+      const int i = min(tid + j * kWriterThreads, rows0 * VPR - 1);
       const int r = i / VPR, c = i % VPR;
       shk[j] = *(const w4*)(krow(D + r) + c * 8);
       shv[j] = *(const w4*)(vrow(D + r) + c * 8);
     }
   }
 
-  // The first aged group's 32 rows go to LDS (the stores below cannot touch
-  // them: phase 1 writes rows >= r0, the shift only after its barrier).
-  auto load_tile = [&](int gi) {
-    for (int i = tid; i < kGroup * VPR; i += kWriterThreads) {
-      const int t = i / VPR, c = i % VPR;
-      k_tile[i] = *(const w4*)(krow(gi * kGroup + t) + c * 8);
-      v_tile[i] = *(const w4*)(vrow(gi * kGroup + t) + c * 8);
-    }
-  };
-  if (D > 0) load_tile(0);
+  if (D > 0) store_tile();
 
   // Every load above lands before any store below (wait + barrier).
   __syncthreads();
@@ -148,10 +185,13 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
     const int lg = old0 / kGroup + gi;
     const int first_page = lg * ppg;
     if (gi > 0) {
+      group_pages(gi, &gp0, &gp1);
       load_tile(gi);
+      store_tile();
       lds_barrier();
     }
     const bool table_ok = first_page + ppg <= g.max_pages;
+    auto phys_of = [&](int k) { return k == 0 ? gp0 : gp1; };  // page k of the group
     const uint16_t* kt = (const uint16_t*)k_tile;
     const uint16_t* vt = (const uint16_t*)v_tile;
     if (tid < 2 * HD) {
@@ -185,7 +225,7 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
         const uint32_t sc = (uint32_t)f2h(s0) | ((uint32_t)f2h(s1) << 16);
         const uint32_t zr = (uint32_t)f2h(mn0) | ((uint32_t)f2h(mn1) << 16);
         for (int pg = 0; pg < ppg; ++pg) {
-          const int phys = bt[first_page + pg];
+          const int phys = phys_of(pg);
           if (phys < 0 || phys >= g.num_pages) continue;
           const int64_t base = ((int64_t)phys * g.nkv + h) * HD + d0;
           *(uint32_t*)(a.k_scale + base) = sc;
@@ -229,7 +269,7 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
       }
       *(w2*)(vcode_tile + t * HDP + cg * (kGroup / 2) + 8 * hf) = w2{packed[0], packed[1]};
       if (hf == 0 && table_ok) {
-        const int phys = bt[first_page + t / P];
+        const int phys = phys_of(t / P);
         if (phys >= 0 && phys < g.num_pages) {
           const int64_t tok = ((int64_t)phys * g.nkv + h) * P + (t % P);
           a.v_scale[tok * HDG + cg] = f2h(sv);
@@ -243,7 +283,7 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
       const int RPC = HDP / 16;  // 16-byte pieces per code row
       for (int i = tid; i < 2 * kGroup * RPC; i += kWriterThreads) {
         const int kv = i / (kGroup * RPC), r = (i / RPC) % kGroup, c = i % RPC;
-        const int phys = bt[first_page + r / P];
+        const int phys = phys_of(r / P);
         if (phys < 0 || phys >= g.num_pages) continue;
         uint8_t* dst = (kv ? a.v_code : a.k_code) +
                        (((int64_t)phys * g.nkv + h) * P + (r % P)) * HDP + 16 * c;
