@@ -287,8 +287,22 @@ __device__ inline void wait_stages(int later) {
 }
 
 // LDS stages per wave: S - 1 groups in flight while one is computed.
-constexpr int kStages = 3;
-static_assert(kStages >= 2 && kStages <= 4, "wait_stages covers up to 3 stages in flight");
+// LDS stages and waves per SIMD of each kernel.  Two waves per SIMD do not
+// hide one wave's dependency chain (LDS read, unpack, QK MFMA chain, max, exp,
+// PV), so the packed HD=128 kernel (G <= 8, the common GQA shapes) runs three
+// per SIMD: at most 168 VGPRs, and two 5 KiB stages per wave so that 12 waves'
+// rings fit the CU's 160 KiB of LDS (one group in flight while one is
+// computed: the memory latency is below a group's compute time).  The other
+// kernels keep three stages; their register use already allows three waves
+// (HD=64) or would spill at three (HD=128, G > 8).
+template <int HD, bool PACK>
+constexpr int stages() {
+  return (HD == 128 && PACK) ? 2 : 3;
+}
+template <int HD, bool PACK>
+constexpr int min_waves_per_simd() {
+  return (HD == 128 && PACK) ? 3 : 1;
+}
 
 // Issue the DMAs of one group whose tokens 0..P-1 sit in page p0 and the
 // rest (page size 16) in p1.
@@ -496,7 +510,6 @@ template <int HD>
 struct SegCtx {
   half8_t qn[HD / 32];  // B operand of Q, natural channel order (bias, residual tiles)
   half8_t qp[HD / 32];  // B operand of Q in the unpack order, odd channels / 16
-  half8_t qm[HD / 32];  // packed mode: qp in columns 8-15 (lo), zero in columns 0-7 (hi)
 };
 
 // QK^T of one quantised group (already in LDS) and its online-softmax update:
@@ -520,27 +533,25 @@ __device__ inline half8_t qk_softmax(WaveState<HD>& st, const SegCtx<HD>& q,
     // G <= 8: columns 0-7 carry q*s (hi) of heads 0-7, columns 8-15 the
     // rounding remainder (lo) of the same heads, so one MFMA does both; a
     // row_ror:8 add merges the halves (and leaves the sum in both lanes).
-    // fma(q, s, -(qm * s)): round(q * s) where qm = 0 (hi), the exact
-    // remainder q * s - round(q * s) where qm = q (lo)
-    half8_t bq[KS];
+    // fma(q, s, 0) = round(q * s) in the hi columns, fma(q, s, -round(q * s))
+    // = the exact remainder in the lo columns
+    const bool lo_col = (lane & 15) >= 8;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const uint8_t* kp = &buf->s[2 * (j * (HD / 4) + 8 * ks)];
       const u32x4 sv = *(const u32x4*)kp;
       const u32x4 zv = *(const u32x4*)(kp + 2 * HD);
       const half8_t sp = as_h8(perm_pairs(sv));
-      bq[ks] = __builtin_elementwise_fma(q.qp[ks], sp, -(q.qm[ks] * sp));
+      const half8_t qs = q.qp[ks] * sp;
+      const half8_t bq = __builtin_elementwise_fma(q.qp[ks], sp, lo_col ? -qs : half8_t(0));
       bz = mfma(as_h8(zv), q.qn[ks], bz);  // sum_d z_d q_gd
-      bh = mfma(neg1024, bq[ks], bh);       // -1024 sum_d B_gd (hi | lo)
+      bh = mfma(neg1024, bq, bh);           // -1024 sum_d B_gd (hi | lo)
+      s0 = mfma(as_h8(unpack_codes(kc[0][ks], nb)), bq, s0);
+      s1 = mfma(as_h8(unpack_codes(kc[1][ks], nb)), bq, s1);
     }
     // the bias is added before the hi/lo merge: a DPP add whose source is an
     // MFMA result register is miscompiled (the DPP combiner reads the
     // tuple's first register for every element), one on a VALU result is not
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      s0 = mfma(as_h8(unpack_codes(kc[0][ks], nb)), bq[ks], s0);
-      s1 = mfma(as_h8(unpack_codes(kc[1][ks], nb)), bq[ks], s1);
-    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float t0 = s0[i] + bh[0], t1 = s1[i] + bh[0];
@@ -708,10 +719,12 @@ __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, in
 }
 
 template <int HD, int P, bool PACK>
-__global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, DecodeArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
+    min_waves_per_simd<HD, PACK>()))) void kivi_decode_stream_kernel(KiviGeo g, DecodeArgs a) {
   using C = Cfg<HD, P>;
   constexpr int KS = C::KS, CPL = C::CPL;
-  constexpr int L = stage_loads<HD>(), S = kStages;
+  constexpr int L = stage_loads<HD>(), S = stages<HD, PACK>();
+  static_assert(S >= 2 && S <= 4, "wait_stages covers up to 3 stages in flight");
   __shared__ __attribute__((aligned(16))) StageBuf<HD> ring[S];
 
   const int lane = threadIdx.x, c = lane & 15, j = lane >> 4;
@@ -814,7 +827,6 @@ __global__ __launch_bounds__(64) void kivi_decode_stream_kernel(KiviGeo g, Decod
       const half8_t div = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)0.0625f, (_Float16)0.0625f,
                            (_Float16)1.0f, (_Float16)1.0f, (_Float16)0.0625f, (_Float16)0.0625f};
       q.qp[ks] = as_h8(perm_pairs(v)) * div;
-      q.qm[ks] = (PACK && c >= 8) ? q.qp[ks] : half8_t(0);
     }
     WaveState<HD> st;
 #pragma unroll
