@@ -8,7 +8,7 @@ crosses the residual window), then paged decode attention runs for one query
 token per sequence.  Inputs are synthetic (seeded N(0,1) with outlier K
 channels, BASELINE workload definitions in jacq_amd/workloads.py) and resident
 in HBM before timing starts.  Each step is bracketed by HIP events on the
-stream the kernels run on; a 512 MiB buffer is written before every step so
+stream the kernels run on; a 512 MiB buffer is read (by default) before every step so
 the 256 MiB MALL and the L2 start cold.
 
 Prints ONE JSON line.  `value` is the effective KV bandwidth of the decode
@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--workload", default="qwen14b")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-flush", action="store_true")
+    ap.add_argument("--flush", choices=("read", "write"), default="read",
+                    help="how the 512 MiB cache flush before each step touches its buffer")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the workload, copy MIB MiB device-to-device a few times "
@@ -123,7 +125,8 @@ def main() -> int:
     out = torch.empty((B, w.nh, w.hd), dtype=torch.float32, device=dev)
     lens_before = torch.from_numpy(lens0.astype(np.int32)).to(dev)
     lens_after = lens_before + 1
-    flush = None if args.no_flush else torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    flush = None if args.no_flush else torch.ones(512 << 20, dtype=torch.uint8, device=dev)
+    flush_sink = torch.zeros(1, dtype=torch.int64, device=dev)
     ws_bytes = kivi.lib().jacq_kivi_decode_workspace_size(ctypes_geo(kivi, geo), B)
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
 
@@ -145,7 +148,13 @@ def main() -> int:
                 torch.cuda.synchronize()
                 wall0 = time.perf_counter()
             if flush is not None:
-                flush.fill_(gi & 0xff)
+                # evict the pool from the 256 MiB MALL and the L2s; a read
+                # leaves no dirty lines whose write-back would land in the
+                # timed decode (--flush write rewrites the buffer instead)
+                if args.flush == "read":
+                    flush_sink.add_(flush.view(torch.int64).sum())
+                else:
+                    flush.fill_(gi & 0xff)
             e = evs[i]
             e[0].record(stream)
             cache.append(nk[gi], nv[gi], bt, lens_before)
@@ -215,6 +224,7 @@ def main() -> int:
             "mean_context": float(np.mean(lens0)),
             "pages": num_pages,
             "cold_cache": flush is not None,
+            "cache_flush": None if flush is None else f"{args.flush} 512 MiB before each step",
         },
         "decode_us": {"mean": round(float(dec.mean()) * 1e3, 2),
                       "min": round(float(dec.min()) * 1e3, 2),

@@ -265,14 +265,17 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
   fill_ws(a, g, batch, sp, waves, need > 0 ? ws : nullptr);
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   profile_slot(ev);
-  if (ev[0] && hipEventRecord(ev[0], stream) != hipSuccess)
-    return fail(JACQ_KIVI_EHIP, "hipEventRecord failed");
-  const hipError_t e = use_simple_decode()
-                           ? jacq::launch_decode(g, a, batch, stream, ev[1])
-                           : jacq::launch_decode_mfma(g, a, batch, stream, ev[1]);
+  hipError_t e;
+  if (use_simple_decode()) {
+    if (ev[0] && hipEventRecord(ev[0], stream) != hipSuccess)
+      return fail(JACQ_KIVI_EHIP, "hipEventRecord failed");
+    e = jacq::launch_decode(g, a, batch, stream, ev[1]);
+    if (e == hipSuccess && ev[2] && hipEventRecord(ev[2], stream) != hipSuccess)
+      return fail(JACQ_KIVI_EHIP, "hipEventRecord failed");
+  } else {
+    e = jacq::launch_decode_mfma(g, a, batch, stream, {ev[0], ev[1], ev[2]});
+  }
   if (e != hipSuccess) return fail(JACQ_KIVI_EHIP, "decode launch failed");
-  if (ev[2] && hipEventRecord(ev[2], stream) != hipSuccess)
-    return fail(JACQ_KIVI_EHIP, "hipEventRecord failed");
   return JACQ_KIVI_OK;
 }
 

@@ -33,6 +33,8 @@
 //          lane c owns channels CPL*c .. CPL*c+CPL-1 (one V scale group), so
 //          V = code * s_t + z_t is dequantised with one packed-fp16 FMA per
 //          two values, and sum_t P z_t accumulates in one extra MFMA per group.
+#include <hip/hip_ext.h>
+
 #include <type_traits>
 #include <utility>
 
@@ -1007,30 +1009,38 @@ __global__ __launch_bounds__(256) void kivi_combine_stream_kernel(KiviGeo g, Dec
 }
 
 template <int HD, int P>
-static void launch_one(const KiviGeo& g, const DecodeArgs& a, hipStream_t stream) {
+static void launch_one(const KiviGeo& g, const DecodeArgs& a, hipStream_t stream,
+                       hipEvent_t start, hipEvent_t stop) {
   if (g.gqa <= 8)
-    hipLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, true>), dim3(a.waves), dim3(64), 0,
-                       stream, g, a);
+    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, true>), dim3(a.waves), dim3(64), 0,
+                          stream, start, stop, 0, g, a);
   else
-    hipLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, false>), dim3(a.waves), dim3(64), 0,
-                       stream, g, a);
+    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, false>), dim3(a.waves), dim3(64), 0,
+                          stream, start, stop, 0, g, a);
 }
 
 hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
-                              hipStream_t stream, hipEvent_t between) {
+                              hipStream_t stream, const LaunchEvents& ev) {
+  // Profiling only.  With main_end, the main kernel's start and end are
+  // stamped by the command processor (its own duration, as a kernel trace
+  // reads it); that launch form delays the next kernel by a few microseconds,
+  // so without main_end plain records bracket the decode instead.
+  hipError_t e;
+  const bool split = ev.main_end != nullptr;
+  if (!split && ev.start && (e = hipEventRecord(ev.start, stream)) != hipSuccess) return e;
+  hipEvent_t s0 = split ? ev.start : nullptr, s1 = split ? ev.main_end : nullptr;
   if (g.hd == 128 && g.page == 16)
-    launch_one<128, 16>(g, a, stream);
+    launch_one<128, 16>(g, a, stream, s0, s1);
   else if (g.hd == 128)
-    launch_one<128, 32>(g, a, stream);
+    launch_one<128, 32>(g, a, stream, s0, s1);
   else if (g.page == 16)
-    launch_one<64, 16>(g, a, stream);
+    launch_one<64, 16>(g, a, stream, s0, s1);
   else
-    launch_one<64, 32>(g, a, stream);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (between && (e = hipEventRecord(between, stream)) != hipSuccess) return e;
+    launch_one<64, 32>(g, a, stream, s0, s1);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL(kivi_combine_stream_kernel, dim3(g.nkv, batch), dim3(256), 0, stream, g, a);
-  return hipGetLastError();
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  return ev.end ? hipEventRecord(ev.end, stream) : hipSuccess;
 }
 
 // One resident wavefront per slot: the tile stream is cut into as many runs as

@@ -75,8 +75,15 @@ hipError_t launch_append(const KiviGeo& g, const AppendArgs& a, int batch, hipSt
 // and before the split-K merge (profiling).
 hipError_t launch_decode(const KiviGeo& g, const DecodeArgs& a, int batch, hipStream_t stream,
                          hipEvent_t between = nullptr);
+// Profiling events of the matrix-core decode (each may be null): with
+// main_end, the main kernel's own start and end stamped by the command
+// processor; without it, plain records before the main kernel; `end` is
+// recorded after the split-K merge.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, main_end = nullptr, end = nullptr;
+};
 hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
-                              hipStream_t stream, hipEvent_t between = nullptr);
+                              hipStream_t stream, const LaunchEvents& ev = LaunchEvents());
 // wavefronts the matrix-core decode launches on a device with `cus` CUs:
 // as many as are resident at once
 int decode_stream_waves(const KiviGeo& g, int cus);
