@@ -750,11 +750,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   const float sscale = 1.4426950408889634f / __builtin_sqrtf((float)HD);  // log2(e)/sqrt(HD)
   const int which = lane >> 5, t32 = lane & 31;
 
-  // Issue arbitration favours the older of a SIMD's two waves, which left
-  // alone finishes its run well before the younger.  Each wave drops its
-  // priority at every quarter of its own run, so a wave behind its partner
-  // outranks it and the pair ends closer together.
-  const int n_run = (int)(x1 - x0), q1 = n_run / 4, q2 = n_run / 2, q3 = 3 * n_run / 4;
+  // Issue arbitration favours the oldest of the waves sharing a SIMD, which left
+  // alone finishes its run well before the younger ones.  Each wave drops its
+  // priority at 1/2, 4/5 and 19/20 of its own run, so a wave behind its
+  // partners outranks them and they reach each mark close together; the last
+  // band, where age alone decides again, is short.
+  const int n_run = (int)(x1 - x0), q1 = n_run / 2, q2 = 4 * n_run / 5, q3 = 19 * n_run / 20;
   int done = 0, level = 3;
   __builtin_amdgcn_s_setprio(3);
   auto progress = [&](int units) {
