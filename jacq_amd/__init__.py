@@ -7,4 +7,4 @@ The native library is ``jacq_amd/libjacq_kivi.so`` (``python -m jacq_amd.build``
 """
 from jacq_amd import abi, bindings, layout  # noqa: F401
 
-__all__ = ["abi", "bindings", "layout", "kivi", "workloads"]
+__all__ = ["abi", "bindings", "layout", "kivi", "cache_io", "workloads"]
