@@ -13,15 +13,18 @@ the 256 MiB MALL and the L2 start cold.
 
 Prints ONE JSON line.  `value` is the effective KV bandwidth of the decode
 (algorithmic bytes / decode time, GB/s); the decode time is the GPU time of
-both decode launches (main kernel + split-K merge) from HIP events the library
-records on the launch stream before and after them (jacq_kivi_profile_*), and
-`ms_per_step` is that time per step.  A second pass of the same number of
-steps, continuing the token stream, also records an event between the two
-launches: `roofline.achieved` is its bytes over the main kernel alone, and
-`kernel_us` / `merge_us` come from it (the marker costs a few microseconds, so
-the first pass leaves it out).  `host_bracketed_us` adds the host-side gaps (Python argument checks
-before each launch) seen by events recorded around the Python calls.  The CPU baseline runs the oracle (oracle/, a C restatement of the
-reference path) over the same state on this host's cores.
+the decode launch (one kernel: the stream wavefronts, then the workgroups
+that merge the split-K partials) from HIP events the library records on the
+launch stream before and after it (jacq_kivi_profile_*), and `ms_per_step` is
+that time per step.  A second pass of the same number of steps, continuing the
+token stream, launches the kernel with start / stop events that the command
+processor stamps at the kernel's own start and end: `roofline.achieved` is its
+bytes over that duration, and `kernel_us` comes from it (that launch form
+delays the next kernel by a few microseconds, so the first pass leaves it
+out).  `host_bracketed_us` adds the host-side gaps (Python argument checks
+before each launch) seen by events recorded around the Python calls.  The CPU
+baseline runs the oracle (oracle/, a C restatement of the reference path) over
+the same state on this host's cores.
 """
 from __future__ import annotations
 
@@ -134,9 +137,9 @@ def main() -> int:
 
     def timed_pass(step0: int, split: bool):
         """warmup + steps of (flush, append, decode) from global step step0;
-        the library's events bracket the decode launches (split: also between
-        the main kernel and the merge).  Returns per-step arrays of the timed
-        steps and the wall time."""
+        the library's events bracket the decode launch (split: stamped by the
+        command processor at the kernel's own start and end).  Returns
+        per-step arrays of the timed steps and the wall time."""
         evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)]
                for _ in range(total_steps)]
         torch.cuda.synchronize()
@@ -175,17 +178,17 @@ def main() -> int:
     # pass 1 (the timed region of the contract): events only around each
     # decode, so the figure is the decode exactly as a caller runs it
     dec, _, wgpu, host, wall = timed_pass(0, split=False)
-    # pass 2: the same steps continued with a marker event between the main
-    # kernel and the merge, for the main kernel's own time (roofline)
-    kern, merge, _, _, _ = timed_pass(total_steps, split=True)
+    # pass 2: the same steps continued, the kernel's own start and end
+    # stamped by the command processor (roofline)
+    kern, _, _, _, _ = timed_pass(total_steps, split=True)
 
     def bytes_of(step0):
         return [layout.decode_step_bytes(lens0 + step0 + i + 1, w.nh, w.nkv, w.hd, w.page,
                                          w.residual, w.group)
                 for i in range(args.warmup, total_steps)]
     step_bytes = bytes_of(0)
-    # GPU time of the decode (main kernel + split-K merge) from the events the
-    # library records on the launch stream; host-side gaps before a launch
+    # GPU time of the decode launch from the events the library records on
+    # the launch stream; host-side gaps before a launch
     # (Python argument checks) are excluded, host_bracketed_* keep them
     wr = wgpu
     host_wr, host_dec = host[:, 0], host[:, 1]
@@ -233,7 +236,6 @@ def main() -> int:
         "kernel_us": {"mean": round(float(kern.mean()) * 1e3, 2),
                       "median": round(float(np.median(kern)) * 1e3, 2),
                       "min": round(float(kern.min()) * 1e3, 2)},
-        "merge_us": {"mean": round(float(merge.mean()) * 1e3, 2)},
         "write_us": {"mean": round(float(wr.mean()) * 1e3, 2),
                      "median": round(float(np.median(wr)) * 1e3, 2)},
         "host_bracketed_us": {"decode": round(float(host_dec.mean()) * 1e3, 2),

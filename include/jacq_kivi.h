@@ -224,7 +224,9 @@ size_t jacq_kivi_decode_workspace_size(const jacq_kivi_geometry* geo, int32_t ba
  *   O             [batch, NH, HD] fp32
  * workspace may be NULL (the library then uses its own, allocated once per
  * device and grown on demand) or at least jacq_kivi_decode_workspace_size
- * bytes.  Sequence lengths are clamped to [0, jacq_kivi_max_seq_len] on the
+ * bytes.  Its contents on entry do not matter: the split-K partials a call
+ * stores are tagged with that call's 64-bit launch epoch.  Two calls that
+ * can run at the same time must not share a workspace.  Sequence lengths are clamped to [0, jacq_kivi_max_seq_len] on the
  * device, as the reference kernel clamps (snapshot :74-83). */
 int jacq_kivi_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q,
                      const int32_t* SEQ_LENS, const int32_t* BLOCK_TABLES,
@@ -294,11 +296,14 @@ int32_t jacq_kivi_plan_batched_write(int32_t start_seq_len, int32_t num_new, int
  * profilers).  jacq_kivi_profile_start enables recording for the next
  * max_calls decode calls and max_calls cache-write calls: each records HIP
  * events on its own stream around its kernels.  jacq_kivi_profile_stop
- * disables recording, waits for the events and writes the per-call
- * milliseconds of the decode main kernel and of its split-K merge (at most
- * cap entries); it returns the number of decode calls written or -1.  With
- * split == 0 no event is recorded between the two decode launches (the
- * marker costs a few microseconds): kernel_ms then holds the whole decode and
+ * disables recording, waits for the events and writes, per call (at most cap
+ * entries), the milliseconds of the decode kernel and of what follows it on
+ * the stream until the decode's end event; it returns the number of decode
+ * calls written or -1.  The matrix-core decode is one kernel (its split-K
+ * merge runs in the same launch).  With split != 0 the kernel is launched
+ * with start / stop events stamped at its own start and end (that launch form
+ * delays the next kernel by a few microseconds); with split == 0 plain
+ * records bracket the decode: kernel_ms then holds the whole decode and
  * merge_ms zero.  jacq_kivi_profile_write_ms then writes the per-call
  * milliseconds of the cache-write kernel recorded in the same window. */
 int jacq_kivi_profile_start(int32_t max_calls, int32_t split);

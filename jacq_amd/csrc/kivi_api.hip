@@ -120,6 +120,9 @@ int library_workspace(int dev, size_t bytes, void** out) {
       return fail(JACQ_KIVI_ENOMEM, "hipMalloc of " + std::to_string(want) +
                                          " workspace bytes failed");
     }
+    // zeroed once: no flag of a fresh buffer matches a launch epoch (they start at 1)
+    if (hipMemset(s.ws, 0, want) != hipSuccess)
+      return fail(JACQ_KIVI_EHIP, "hipMemset(workspace) failed");
     s.ws_bytes = want;
   }
   *out = s.ws;
@@ -155,10 +158,13 @@ size_t partial_slots(const KiviGeo& g, int batch, const SplitPlan& sp, int waves
 }
 
 // Workspace: [m,l fp32 per slot and head][acc fp32 per slot, head, channel]
-// and, for the matrix-core kernel, [first, last wavefront int32 per segment].
+// and, for the matrix-core kernel, [epoch uint64 per slot] (8-byte aligned:
+// G * (HD + 2) floats per slot is even).  The flags need no initial contents:
+// a flag counts only when it holds the current launch's 64-bit epoch.
 size_t workspace_bytes(const KiviGeo& g, int batch, const SplitPlan& sp, int waves) {
-  const size_t seg = use_simple_decode() ? 0 : (size_t)batch * g.nkv * 2 * sizeof(int32_t);
-  return partial_slots(g, batch, sp, waves) * g.gqa * (size_t)(g.hd + 2) * sizeof(float) + seg;
+  const size_t slots = partial_slots(g, batch, sp, waves);
+  const size_t flags = use_simple_decode() ? 0 : slots * sizeof(uint64_t);
+  return slots * g.gqa * (size_t)(g.hd + 2) * sizeof(float) + flags;
 }
 
 void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& sp, int waves,
@@ -169,7 +175,7 @@ void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& 
   const size_t slots = partial_slots(g, batch, sp, waves) * g.gqa;
   a.ws_ml = (float*)ws;
   a.ws_acc = ws ? a.ws_ml + slots * 2 : nullptr;
-  a.ws_seg = ws ? (int32_t*)(a.ws_acc + slots * g.hd) : nullptr;
+  a.ws_flag = ws ? (uint64_t*)(a.ws_acc + slots * g.hd) : nullptr;
 }
 
 // ---- measurement hook: HIP events around the two decode launches ----

@@ -8,8 +8,8 @@
 // resident for its whole run (no per-split prologue), and prefetches the next
 // tile's block-table entries (scalar loads) and bytes while it computes the
 // current one.  A run that covers a whole (sequence, kv head) writes O
-// directly; otherwise it leaves an online-softmax partial (m, l, acc) that
-// kivi_combine_stream_kernel merges with the log-sum-exp rule of the
+// directly; otherwise it leaves an online-softmax partial (m, l, acc) that the
+// merge workgroups of the same launch combine with the log-sum-exp rule of the
 // reference's split-K decode (crates/jac-codegen-cuda/src/variants.rs:3548-3565).
 //
 // All G query heads of a kv head share each tile: they form the 16-wide N
@@ -35,6 +35,8 @@
 //          two values, and sum_t P z_t accumulates in one extra MFMA per group.
 #include <hip/hip_ext.h>
 
+#include <algorithm>
+#include <atomic>
 #include <type_traits>
 #include <utility>
 
@@ -720,6 +722,202 @@ __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, in
   return rt;
 }
 
+// ---- split-K merge, run by workgroups of the same launch ----
+//
+// The stream wavefronts fill every slot of the device, so the merge
+// workgroups (block ids past a.waves) start as stream wavefronts finish, on
+// the CUs the end of the launch leaves idle.  A wavefront that leaves a
+// partial stores it with agent-scope stores (they reach the point of
+// coherence of all XCDs without an L2 write-back), waits for them, and then
+// stores the launch's 64-bit epoch in the partial's flag.  A merge wavefront
+// reads a partial only after it has read that epoch from the flag, with
+// agent-scope loads.  Flags of earlier launches or of a fresh buffer hold
+// another value, so the workspace needs no reset.  The merge does not hold
+// anything a stream wavefront waits for, and there are at most half as many
+// merge workgroups as stream slots, so the stream wavefronts always run; a
+// merge wavefront that still waits after kMergeTimeoutTicks (s_memrealtime,
+// 100 MHz) writes NaN for its segments and ends, so the launch always drains.
+constexpr uint64_t kMergeTimeoutTicks = 100000000;  // 1 s
+
+// Global unit index of (b, kv head 0): NKV times the units of the sequences before b.
+__device__ inline int64_t seq_start(const KiviGeo& g, const DecodeArgs& a, int b, int lane) {
+  int64_t run = 0;
+  for (int base = 0; base < b; base += 64) {
+    const int bb = base + lane;
+    const int U = bb < b ? seq_units(g, a, bb) : 0;
+    run += __builtin_amdgcn_readfirstlane(wave_sum_i(U));
+  }
+  return run * g.nkv;
+}
+
+// First unit of wavefront w's run, and the wavefront whose run holds unit x.
+__device__ inline int64_t run_begin(int64_t w, int64_t TT, int64_t W) { return w * TT / W; }
+__device__ inline int64_t wave_of(int64_t x, int64_t TT, int64_t W) {
+  int64_t w = x * W / TT;
+  while (w > 0 && run_begin(w, TT, W) > x) --w;
+  while (w + 1 < W && run_begin(w + 1, TT, W) <= x) ++w;
+  return w;
+}
+
+__device__ inline uint64_t ld_agent(const void* p) {
+  return __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st_agent(void* p, float lo, float hi) {
+  const uint64_t v = (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
+  __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16-byte agent-scope store (the bits the compiler gives an agent-scope
+// relaxed atomic store, sc1, on a four-dword store); waited for by the
+// explicit vmcnt(0) before the partial's flag
+__device__ inline void st_agent4(float* p, floatx4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+// 16-byte agent-scope load; the caller waits with an explicit vmcnt(0) and
+// then passes the value through keep() so no use moves above the wait
+__device__ inline floatx4 ld_agent4(const float* p) {
+  floatx4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ inline void keep(floatx4& v) { asm volatile("" : "+v"(v)); }
+__device__ inline float lo_f(uint64_t v) { return __uint_as_float((uint32_t)v); }
+__device__ inline float hi_f(uint64_t v) { return __uint_as_float((uint32_t)(v >> 32)); }
+
+// Log-sum-exp merge of the partials of every (sequence, kv head) whose run was
+// cut (variants.rs:3548-3565): M = max m_w, L = sum l_w e^(m_w - M), acc
+// likewise, O = acc / max(L, 1e-30), in the log2 domain of the decode loop.
+// The pieces of a segment are recomputed from the same split the stream
+// wavefronts used; a segment with a single non-empty piece was written whole.
+template <int HD, bool PACK>
+__device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) {
+  constexpr int K = (PACK ? 8 : 16) * HD / 256;  // float4 outputs per lane: G * HD <= 256 K
+  constexpr int U = K > 4 ? 1 : 2;               // partials whose loads are in flight together
+  const int G = g.gqa, NKV = g.nkv, n4 = G * HD / 4;
+  const int64_t TT = stream_units(g, a, lane);
+  const int64_t W = stream_waves(TT, a.waves);
+  const int nseg = a.batch * NKV;
+  const uint64_t epoch = a.epoch, t_start = __builtin_amdgcn_s_memrealtime();
+  bool late = false;  // wave-uniform: the wait ran out
+  int gi[K], d[K];
+  bool on[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int e = lane + 64 * k;  // outputs 4e .. 4e + 3 of head gi
+    on[k] = e < n4;
+    gi[k] = 4 * e / HD;
+    d[k] = 4 * e - gi[k] * HD;
+  }
+  for (int seg = (int)blockIdx.x - a.waves; seg < nseg; seg += a.merge_wgs) {
+    const int b = seg / NKV, h = seg - b * NKV;
+    int ov, n;
+    const int T = seq_tiles(g, a, b, &ov, &n);
+    const int nq = ov / kGroup;
+    const int units = nq + kResidualUnits * (T - nq);
+    const int64_t S0 = seq_start(g, a, b, lane) + (int64_t)h * units, S1 = S0 + units;
+    const int64_t w0 = wave_of(S0, TT, W), w1 = wave_of(S1 - 1, TT, W);
+    // non-empty pieces: the runs that own at least one tile of the segment
+    auto owns = [&](int64_t w) {
+      const int64_t x0 = max(run_begin(w, TT, W), S0), x1 = min(run_begin(w + 1, TT, W), S1);
+      return tile_at((int)(x0 - S0), nq) < tile_at((int)(x1 - S0), nq);
+    };
+    int pieces = 0;
+    for (int64_t wb = w0; wb <= w1; wb += 64)
+      pieces += __builtin_popcountll(
+          __builtin_amdgcn_ballot_w64(wb + lane <= w1 && owns(wb + lane)));
+    if (pieces <= 1) continue;  // written whole by its wavefront
+
+    float M[K], Lsum[K];
+    floatx4 acc[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      M[k] = -INFINITY;
+      Lsum[k] = 0.0f;
+      acc[k] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int64_t wb = w0; wb <= w1 && !late; wb += 64) {
+      const int64_t wl = wb + lane;
+      const bool mine = wl <= w1 && owns(wl);
+      const uint64_t* flag = a.ws_flag + seg + wl;
+      uint64_t todo = __builtin_amdgcn_ballot_w64(mine);
+      // fold the partials in piece order (the result does not depend on
+      // timing), each run of them as soon as its flags show this launch's
+      // epoch: after the last one lands, only those behind it remain
+      while (todo) {
+        const uint64_t bit = 1ull << lane;
+        // one lane waits for the first piece in order ...
+        if (lane == __builtin_ctzll(todo)) {
+          while (ld_agent(flag) != epoch &&
+                 __builtin_amdgcn_s_memrealtime() - t_start <= kMergeTimeoutTicks)
+            __builtin_amdgcn_s_sleep(4);
+        }
+        // ... then one round finds how many after it have landed too
+        const uint64_t landed =
+            __builtin_amdgcn_ballot_w64((todo & bit) && ld_agent(flag) == epoch);
+        // the ready prefix: pieces of todo below its first one not yet stored
+        const uint64_t waiting = todo & ~landed;
+        uint64_t ready = waiting ? todo & ((waiting & (0 - waiting)) - 1) : todo;
+        if (!ready) {  // the first piece's wait ran out
+          late = true;
+          break;
+        }
+        todo &= ~ready;
+        while (ready) {
+          int64_t slot[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            slot[u] = -1;
+            if (ready) {
+              slot[u] = seg + wb + __builtin_ctzll(ready);
+              ready &= ready - 1;
+            }
+          }
+          uint64_t ml[U][K];
+          floatx4 vv[U][K];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+              ml[u][k] = 0xff800000u;  // (m, l) = (-inf, 0): folded with weight 0
+              vv[u][k] = floatx4{0.f, 0.f, 0.f, 0.f};
+              if (slot[u] >= 0 && on[k]) {
+                const int64_t p = slot[u] * G + gi[k];
+                ml[u][k] = ld_agent(a.ws_ml + 2 * p);
+                vv[u][k] = ld_agent4(a.ws_acc + p * HD + d[k]);
+              }
+            }
+          }
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int k = 0; k < K; ++k) keep(vv[u][k]);
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+              const float m = lo_f(ml[u][k]), l = hi_f(ml[u][k]);
+              const float mn = fmaxf(M[k], m);
+              const float fo = __builtin_amdgcn_exp2f(M[k] - mn);
+              const float fn = __builtin_amdgcn_exp2f(m - mn);
+              const floatx4 v = vv[u][k];
+              acc[k] = acc[k] * fo + v * fn;
+              Lsum[k] = Lsum[k] * fo + l * fn;
+              M[k] = mn;
+            }
+          }
+        }
+      }
+    }
+    float* out = a.out + (int64_t)b * a.out_stride + (int64_t)h * G * HD;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (on[k])
+        *(floatx4*)(out + (int64_t)gi[k] * HD + d[k]) =
+            late ? floatx4{NAN, NAN, NAN, NAN} : acc[k] / fmaxf(Lsum[k], 1.0e-30f);
+  }
+}
+
 template <int HD, int P, bool PACK>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     min_waves_per_simd<HD, PACK>()))) void kivi_decode_stream_kernel(KiviGeo g, DecodeArgs a) {
@@ -730,9 +928,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   __shared__ __attribute__((aligned(16))) StageBuf<HD> ring[S];
 
   const int lane = threadIdx.x, c = lane & 15, j = lane >> 4;
+  if ((int)blockIdx.x >= a.waves) {
+    merge_segments<HD, PACK>(g, a, lane);
+    return;
+  }
   const int G = g.gqa, NKV = g.nkv;
   const int64_t TT = stream_units(g, a, lane);
-  const int64_t W = stream_waves(TT, gridDim.x);
+  const int64_t W = stream_waves(TT, a.waves);
   const int w = blockIdx.x;
   if (w >= W) return;
   const int64_t x0 = (int64_t)w * TT / W, x1 = (int64_t)(w + 1) * TT / W;
@@ -777,6 +979,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   int kvh = (int)((x0 - sp.start) / sp.units);
   int u = (int)((x0 - sp.start) % sp.units);  // unit offset inside the segment
   int64_t x = x0;
+  int64_t cut_first = -1, cut_last = -1;  // pieces this run leaves as partials
   while (x < x1) {
     const int b = sp.b, h = kvh;
     int ov, n;
@@ -897,7 +1100,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
       progress(kResidualUnits);
     }
 
-    // ---- segment output: O directly, or a partial for the combine kernel ----
+    // ---- segment output: O directly, or a partial for the merge workgroups ----
     // row sums: Sigma P of O row 4j + i sits in the sum column C1 of row
     // block j; a sum lane takes its group's Sigma P z from its left neighbour
     const bool whole = (t_beg == 0 && t_fin == T);
@@ -912,6 +1115,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     }
     float* dst = whole ? a.out + (int64_t)b * a.out_stride + (int64_t)h * G * HD
                        : a.ws_acc + piece * G * HD;
+    // the lane's output offset, computed here: hoisted out of the segment
+    // loop it would hold two registers for the whole run
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int lane_off = (ln >> 4) * 4 * HD + CPL * (ln & 15);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 4 * j + i;
@@ -919,113 +1127,84 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
         float v[CPL];
 #pragma unroll
         for (int nt = 0; nt < CPL; ++nt) v[nt] = (st.o[nt][i] + zsum[i]) * rowscale[i];
-        float* p = dst + (int64_t)row * HD + CPL * c;
+        float* p = dst + lane_off + i * HD;
+        if (whole) {
 #pragma unroll
-        for (int q4 = 0; q4 < CPL / 4; ++q4)
-          *(floatx4*)(p + 4 * q4) = floatx4{v[4 * q4], v[4 * q4 + 1], v[4 * q4 + 2], v[4 * q4 + 3]};
-      }
-    }
-    float lh[4];  // Sigma P of head c (rows 4 (c >> 2) + i)
+          for (int q4 = 0; q4 < CPL / 4; ++q4)
+            *(floatx4*)(p + 4 * q4) =
+                floatx4{v[4 * q4], v[4 * q4 + 1], v[4 * q4 + 2], v[4 * q4 + 3]};
+        } else if (CPL == 4) {  // read by a merge wavefront, possibly on another XCD
+          st_agent4(p, floatx4{v[0], v[1], v[2], v[3]});
+        } else {
+          // agent-scope stores bypass the L2, so each instruction should
+          // write whole sectors: lane c of the row's 16 takes floats
+          // 4c .. 4c + 3 and then 64 + 4c .. 64 + 4c + 3 (held by lanes c / 2
+          // and 8 + c / 2, half c % 2), two 256-byte contiguous stores
+          float* row_base = dst + (((ln >> 4) << 2) + i) * HD;
+          const int cl = ln & 15, src0 = (ln & 48) + (cl >> 1), hi = cl & 1;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) lh[i] = __shfl(st.ob[i], 16 * (c >> 2) + C1, 64);
-    if (!whole && j == 0 && c < G) {
-      const int ci = c & 3;
-      a.ws_ml[(piece * G + c) * 2] = st.m;
-      a.ws_ml[(piece * G + c) * 2 + 1] = ci == 0 ? lh[0] : ci == 1 ? lh[1] : ci == 2 ? lh[2] : lh[3];
-    }
-    if (lane == 0) {  // the combine kernel's map: first and last wavefront of the segment
-      const int64_t seg = (int64_t)b * NKV + h;
-      if (t_beg == 0) a.ws_seg[2 * seg] = w;
-      if (t_fin == T) a.ws_seg[2 * seg + 1] = w;
-    }
-  }
-}
-
-// Log-sum-exp merge of the partials of one (sequence, kv head) left by the
-// wavefronts whose runs cut it (variants.rs:3548-3565).  One workgroup per
-// (kv head, sequence); a separate launch, so every partial is visible across
-// the GPU's L2 slices without device-scope fences in the decode kernel.  The
-// decode kernel records the first and last wavefront of every segment, so a
-// segment that one wavefront finished costs a single scalar load here, and a
-// cut one loads all of its partials at once.
-__global__ __launch_bounds__(256) void kivi_combine_stream_kernel(KiviGeo g, DecodeArgs a) {
-  constexpr int K = 2;  // float4 outputs per thread: G * HD <= 16 * 128 = 2048 = 256 * K * 4
-  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int G = g.gqa, HD = g.hd, NKV = g.nkv, n4 = G * HD / 4;
-  const int64_t seg = (int64_t)b * NKV + h;
-  const __attribute__((address_space(4))) int32_t* sw =
-      (const __attribute__((address_space(4))) int32_t*)a.ws_seg;
-  const int w0 = sw[2 * seg], w1 = sw[2 * seg + 1];
-  if (w0 >= w1) return;  // written whole by the decode kernel
-  int gi[K], d[K];
-  bool on[K];
-  floatx4 acc[K];
-  float M[K], L[K];
+          for (int part = 0; part < 2; ++part) {
+            const int src = src0 + 8 * part;
+            floatx4 o;
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int e = tid + 256 * k;  // outputs 4e .. 4e + 3 of one head (HD % 4 == 0)
-    on[k] = e < n4;
-    gi[k] = 4 * e / HD;
-    d[k] = 4 * e - gi[k] * HD;
-    M[k] = -INFINITY;
-    L[k] = 0.0f;
-    acc[k] = floatx4{0.f, 0.f, 0.f, 0.f};
-  }
-  // the loads of U partials are issued before the first is used: a segment's
-  // few partials cost one or two memory latencies, not one each
-  constexpr int U = 4;
-  for (int w = w0; w <= w1; w += U) {
-    float2 ml[U][K];
-    floatx4 v[U][K];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        ml[u][k] = float2{-INFINITY, 0.0f};  // past the end: folded with weight 0
-        v[u][k] = floatx4{0.f, 0.f, 0.f, 0.f};
-        if (on[k] && w + u <= w1) {
-          const int64_t p = (seg + w + u) * G + gi[k];
-          ml[u][k] = *(const float2*)(a.ws_ml + 2 * p);
-          v[u][k] = *(const floatx4*)(a.ws_acc + p * HD + d[k]);
+            for (int e = 0; e < 4; ++e) {
+              const float lo_half = __shfl(v[e], src, 64), hi_half = __shfl(v[4 + e], src, 64);
+              o[e] = hi ? hi_half : lo_half;
+            }
+            st_agent4(row_base + 64 * part + 4 * cl, o);
+          }
         }
       }
     }
+    if (!whole) {
+      float lh[4];  // Sigma P of head c (rows 4 (c >> 2) + i)
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        const float mn = fmaxf(M[k], ml[u][k].x);
-        const float fo = __builtin_amdgcn_exp2f(M[k] - mn);
-        const float fn = __builtin_amdgcn_exp2f(ml[u][k].x - mn);
-        acc[k] = acc[k] * fo + v[u][k] * fn;
-        L[k] = L[k] * fo + ml[u][k].y * fn;
-        M[k] = mn;
+      for (int i = 0; i < 4; ++i) lh[i] = __shfl(st.ob[i], 16 * (c >> 2) + C1, 64);
+      if (j == 0 && c < G) {
+        const int ci = c & 3;
+        st_agent(a.ws_ml + (piece * G + c) * 2, st.m,
+                 ci == 0 ? lh[0] : ci == 1 ? lh[1] : ci == 2 ? lh[2] : lh[3]);
       }
+      // only a run's first and last segments can be cut
+      (t_beg == 0 ? cut_last : cut_first) = piece;
     }
   }
-  float* out = a.out + (int64_t)b * a.out_stride + (int64_t)h * G * HD;
-#pragma unroll
-  for (int k = 0; k < K; ++k)
-    if (on[k]) *(floatx4*)(out + (int64_t)gi[k] * HD + d[k]) = acc[k] / fmaxf(L[k], 1.0e-30f);
+  // flags after the run: the partials are complete at the point of coherence
+  // before their flags are
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (lane == 0) {
+    if (cut_first >= 0)
+      __hip_atomic_store(a.ws_flag + cut_first, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (cut_last >= 0)
+      __hip_atomic_store(a.ws_flag + cut_last, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 template <int HD, int P>
 static void launch_one(const KiviGeo& g, const DecodeArgs& a, hipStream_t stream,
                        hipEvent_t start, hipEvent_t stop) {
+  const dim3 grid(a.waves + a.merge_wgs);
   if (g.gqa <= 8)
-    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, true>), dim3(a.waves), dim3(64), 0,
-                          stream, start, stop, 0, g, a);
+    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, true>), grid, dim3(64), 0, stream,
+                          start, stop, 0, g, a);
   else
-    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, false>), dim3(a.waves), dim3(64), 0,
-                          stream, start, stop, 0, g, a);
+    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, false>), grid, dim3(64), 0, stream,
+                          start, stop, 0, g, a);
 }
 
-hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
+hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& args, int batch,
                               hipStream_t stream, const LaunchEvents& ev) {
-  // Profiling only.  With main_end, the main kernel's start and end are
-  // stamped by the command processor (its own duration, as a kernel trace
-  // reads it); that launch form delays the next kernel by a few microseconds,
-  // so without main_end plain records bracket the decode instead.
+  // One launch: the stream wavefronts, then the merge workgroups (at most
+  // half as many as stream slots, each taking segments in turn).  Every
+  // launch gets its own epoch, which marks the partials it stores.
+  static std::atomic<uint64_t> epochs{0};
+  DecodeArgs a = args;
+  a.epoch = epochs.fetch_add(1, std::memory_order_relaxed) + 1;
+  a.merge_wgs = std::max(1, std::min(batch * g.nkv, a.waves / 2));
+  // Profiling only.  With main_end, the kernel's start and end are stamped by
+  // the command processor (its own duration, as a kernel trace reads it);
+  // that launch form delays the next kernel by a few microseconds, so without
+  // main_end a plain record precedes the launch instead.
   hipError_t e;
   const bool split = ev.main_end != nullptr;
   if (!split && ev.start && (e = hipEventRecord(ev.start, stream)) != hipSuccess) return e;
@@ -1038,8 +1217,6 @@ hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
     launch_one<64, 16>(g, a, stream, s0, s1);
   else
     launch_one<64, 32>(g, a, stream, s0, s1);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(kivi_combine_stream_kernel, dim3(g.nkv, batch), dim3(256), 0, stream, g, a);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   return ev.end ? hipEventRecord(ev.end, stream) : hipSuccess;
 }

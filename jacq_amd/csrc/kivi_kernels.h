@@ -45,10 +45,12 @@ struct DecodeArgs {
   int64_t out_stride;
   float* ws_ml;   // [batch, NKV, max_splits, G, 2]  (m, l)
   float* ws_acc;  // [batch, NKV, max_splits, G, HD]
-  int32_t* ws_seg;  // matrix-core kernel: [batch, NKV, 2] first / last wavefront of a segment
+  uint64_t* ws_flag;  // matrix-core kernel: per partial slot, the epoch of the launch that stored it
   int max_splits;  // VALU kernel: split slots per (sequence, kv head)
   int batch;       // sequences (queries) in the call
   int waves;       // matrix-core kernel: wavefronts sharing the tile stream
+  int merge_wgs = 0;       // matrix-core kernel: merge workgroups after the stream wavefronts
+  uint64_t epoch = 0;      // matrix-core kernel: this launch's tag (set by the launcher)
   int retained_pages = -1;  // >= 0: sparse-retained window (compact block table)
 };
 
@@ -76,9 +78,8 @@ hipError_t launch_append(const KiviGeo& g, const AppendArgs& a, int batch, hipSt
 hipError_t launch_decode(const KiviGeo& g, const DecodeArgs& a, int batch, hipStream_t stream,
                          hipEvent_t between = nullptr);
 // Profiling events of the matrix-core decode (each may be null): with
-// main_end, the main kernel's own start and end stamped by the command
-// processor; without it, plain records before the main kernel; `end` is
-// recorded after the split-K merge.
+// main_end, the kernel's own start and end stamped by the command processor;
+// without it, a plain record before the kernel; `end` is recorded after it.
 struct LaunchEvents {
   hipEvent_t start = nullptr, main_end = nullptr, end = nullptr;
 };

@@ -158,7 +158,8 @@ def profile_start(max_calls: int, split: bool = True) -> None:
 
 
 def profile_stop(cap: int = 4096):
-    """(main-kernel ms, merge ms) per recorded decode call, in call order."""
+    """(kernel ms, ms after the kernel until the decode's end event) per
+    recorded decode call, in call order."""
     k = (ctypes.c_float * cap)()
     m = (ctypes.c_float * cap)()
     n = lib().jacq_kivi_profile_stop(k, m, cap)
