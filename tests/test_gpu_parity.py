@@ -319,3 +319,34 @@ def test_decode_extreme_value_scales(kivi):
         bound = 2e-3 + 1e-2 * np.abs(ref[b]) + 2.0 ** -10 * mag
         err = np.abs(got[b] - ref[b])
         assert (err <= bound).all(), f"seq {b}: worst excess {(err - bound).max():.3e}"
+
+
+def test_caller_workspace_needs_no_initial_contents(kivi):
+    """A caller workspace filled with random bytes, then reused by a second
+    call with other queries, decodes to the same bits as the library's own
+    workspace: the merge reads only partials tagged with its own launch."""
+    w = wl.WORKLOADS["qwen14b"]
+    st = State(w, lens=[3000, 700, 5001, 129], seed=21)
+    st.build_oracle()
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, st.max_pages,
+                            st.num_pages)
+    cache = kivi.PagedKiviCache.from_tensors(geo, to_torch(st))
+    lens = torch.from_numpy(st.lens.astype(np.int32)).cuda()
+    bt = torch.from_numpy(st.tables).cuda()
+    q1 = torch.from_numpy(st.q).view(torch.float16).cuda()
+    q2 = torch.randn(q1.shape, generator=torch.Generator(device="cuda").manual_seed(3),
+                     device="cuda").half()
+    ref1, ref2 = cache.decode(q1, lens, bt), cache.decode(q2, lens, bt)
+    nbytes = kivi.lib().jacq_kivi_decode_workspace_size(ctypes_geo(kivi, geo), st.batch)
+    ws = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda")
+    got1 = cache.decode(q1, lens, bt, workspace=ws)
+    got2 = cache.decode(q2, lens, bt, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(got1.view(torch.int32), ref1.view(torch.int32))
+    assert torch.equal(got2.view(torch.int32), ref2.view(torch.int32))
+    assert_close(got1.cpu().numpy(), st.decode_ref(), "random workspace")
+
+
+def ctypes_geo(kivi, geo):
+    import ctypes
+    return ctypes.byref(geo.c())

@@ -326,3 +326,23 @@ def test_sparse_retained_entry_point_rejects_like_reference(native):
     assert native.jacq_kivi_decode_sparse_retained(ctypes.byref(small), ok, 4096, ok, 11,
                                                    *caches, ok, None, 0, None) == 1
     assert b"physical page storage" in native.jacq_kivi_last_error()
+
+
+def test_build_spill_guard_parses_resource_remarks():
+    """The build rejects a stream / writer kernel that spills (scratch makes the
+    decode ~13% slower); the guard reads the compiler's resource remarks."""
+    from jacq_amd import build as b
+    remarks = "\n".join([
+        "x.hip:1:1: remark: Function Name: _ZN4jacq25kivi_decode_stream_kernelILi128ELi16ELb1EEEvNS_7KiviGeoENS_10DecodeArgsE [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     VGPRs: 161 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     ScratchSize [bytes/lane]: 12 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     Occupancy [waves/SIMD]: 3 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark: Function Name: _ZN4jacq18kivi_append_kernelENS_7KiviGeoENS_10AppendArgsE [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark:     VGPRs: 90 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    r = b.kernel_resources(remarks)
+    stream = [v for k, v in r.items() if "kivi_decode_stream_kernel" in k][0]
+    assert stream == {"vgprs": 161, "scratch": 12, "occupancy": 3}
+    append = [v for k, v in r.items() if "kivi_append_kernel" in k][0]
+    assert append["scratch"] == 0
