@@ -178,11 +178,14 @@ void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& 
   a.ws_flag = ws ? (uint64_t*)(a.ws_acc + slots * g.hd) : nullptr;
 }
 
-// ---- measurement hook: HIP events around the two decode launches ----
+// ---- measurement hook: HIP events around the decode ----
 // While enabled, each decode call takes the next triple of a pre-created
-// event pool and records it on the call's own stream: before the main
-// kernel, between it and the split-K merge (split mode only: the marker
-// itself costs a few microseconds), and after the merge.
+// event pool and uses it on the call's own stream: before the decode, a
+// middle event in split mode only, and after the decode.  In split mode the
+// matrix-core decode (one kernel) is launched with the first two as the
+// start / stop events the command processor stamps at the kernel's own start
+// and end; the VALU decode records the middle one between its kernel and its
+// merge.  Split mode delays the next kernel by a few microseconds.
 struct Profiler {
   bool on = false;
   bool split = true;

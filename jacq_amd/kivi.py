@@ -151,8 +151,10 @@ def last_error() -> str:
 
 
 def profile_start(max_calls: int, split: bool = True) -> None:
-    """Record HIP events around the next max_calls decode calls; with split,
-    also between the main kernel and the merge."""
+    """Record HIP events around the next max_calls decode calls.  With split,
+    the matrix-core decode (one kernel) is launched with start / stop events
+    stamped at the kernel's own start and end; the VALU decode records an event
+    between its kernel and its merge."""
     if lib().jacq_kivi_profile_start(max_calls, int(split)) != 0:
         raise KiviLaunchError(last_error())
 
