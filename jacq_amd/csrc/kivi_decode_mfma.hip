@@ -648,9 +648,12 @@ __device__ inline int64_t stream_units(const KiviGeo& g, const DecodeArgs& a, in
   return tot * g.nkv;
 }
 
-// Wavefronts that share the stream: at most gridDim.x, and at least
-// kMinUnitsPerWave units each so that tiny batches do not scatter.
-constexpr int kMinUnitsPerWave = 8;
+// Wavefronts that share the stream: at most the resident ones, and at least
+// kMinUnitsPerWave units each, so that small batches spread over enough
+// wavefronts to hide the per-group latency chain without cutting every
+// segment into pieces the merge must fold (4: TinyLlama 17.9 -> 15.6 us,
+// Qwen0.5B 19.6 -> 18.5 us against 8; 2 was slower at Qwen0.5B).
+constexpr int kMinUnitsPerWave = 4;
 __device__ inline int64_t stream_waves(int64_t units, int grid) {
   int64_t w = (units + kMinUnitsPerWave - 1) / kMinUnitsPerWave;
   if (w < 1) w = 1;
@@ -791,7 +794,7 @@ __device__ inline float hi_f(uint64_t v) { return __uint_as_float((uint32_t)(v >
 template <int HD, bool PACK>
 __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) {
   constexpr int K = (PACK ? 8 : 16) * HD / 256;  // float4 outputs per lane: G * HD <= 256 K
-  constexpr int U = K > 4 ? 1 : 2;               // partials whose loads are in flight together
+  constexpr int U = K <= 2 ? 8 : K > 4 ? 1 : 2;  // partials whose loads are in flight together
   const int G = g.gqa, NKV = g.nkv, n4 = G * HD / 4;
   const int64_t TT = stream_units(g, a, lane);
   const int64_t W = stream_waves(TT, a.waves);
