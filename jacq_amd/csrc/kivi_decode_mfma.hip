@@ -313,7 +313,6 @@ constexpr int min_waves_per_simd() {
 template <int HD, int P>
 __device__ inline void load_stage(StageBuf<HD>* buf, const StageBases& sb, uint32_t p0,
                                   uint32_t p1, int lane) {
-  using C = Cfg<HD, P>;
   const uint32_t base = lds_addr(buf);
   const uint32_t kd = base + (uint32_t)offsetof(StageBuf<HD>, k);
   const uint32_t vd = base + (uint32_t)offsetof(StageBuf<HD>, v);
@@ -936,7 +935,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     return;
   }
   const int G = g.gqa, NKV = g.nkv;
-  const int64_t TT = stream_units(g, a, lane);
+  // Up to 64 sequences, one length load per lane serves the stream's total,
+  // the run's first sequence and that sequence's window: the first block-table
+  // read waits for one memory round, not three.
+  const bool one_pass = a.batch <= 64;
+  int lane_T = 0, lane_ov = 0, lane_n = 0, lane_U = 0;
+  if (one_pass && lane < a.batch) {
+    lane_T = seq_tiles(g, a, lane, &lane_ov, &lane_n);
+    lane_U = lane_ov / kGroup + kResidualUnits * (lane_T - lane_ov / kGroup);
+  }
+  const int lane_incl = wave_incl_scan(lane_U, lane);
+  const int64_t TT = one_pass ? (int64_t)NKV * __builtin_amdgcn_readlane(lane_incl, 63)
+                              : stream_units(g, a, lane);
   const int64_t W = stream_waves(TT, a.waves);
   const int w = blockIdx.x;
   if (w >= W) return;
@@ -953,7 +963,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     for (int s_ = 0; s_ < S; ++s_) ((uint32_t*)ring[s_].ones)[lane] = 0x3C003C00u;
   }
   const float sscale = 1.4426950408889634f / __builtin_sqrtf((float)HD);  // log2(e)/sqrt(HD)
-  const int which = lane >> 5, t32 = lane & 31;
 
   // Issue arbitration favours the oldest of the waves sharing a SIMD, which left
   // alone finishes its run well before the younger ones.  Each wave drops its
@@ -978,15 +987,30 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
       level = 0;
     }
   };
-  SeqSpan sp = locate(g, a, x0, lane);
+  SeqSpan sp;
+  int first_T = 0, first_ov = 0, first_n = 0;  // the first segment's window (one_pass)
+  if (one_pass) {
+    const uint64_t hit =
+        __builtin_amdgcn_ballot_w64(lane < a.batch && (int64_t)NKV * lane_incl > x0);
+    const int f = __builtin_ctzll(hit);  // x0 < TT: some lane hits
+    const int Uf = __builtin_amdgcn_readlane(lane_U, f);
+    sp = {f, (int64_t)NKV * (__builtin_amdgcn_readlane(lane_incl, f) - Uf), Uf};
+    first_T = __builtin_amdgcn_readlane(lane_T, f);
+    first_ov = __builtin_amdgcn_readlane(lane_ov, f);
+    first_n = __builtin_amdgcn_readlane(lane_n, f);
+  } else {
+    sp = locate(g, a, x0, lane);
+  }
+  bool first_seg = one_pass;
   int kvh = (int)((x0 - sp.start) / sp.units);
   int u = (int)((x0 - sp.start) % sp.units);  // unit offset inside the segment
   int64_t x = x0;
   int64_t cut_first = -1, cut_last = -1;  // pieces this run leaves as partials
   while (x < x1) {
     const int b = sp.b, h = kvh;
-    int ov, n;
-    const int T = seq_tiles(g, a, b, &ov, &n);
+    int ov = first_ov, n = first_n, T = first_T;
+    if (!first_seg) T = seq_tiles(g, a, b, &ov, &n);
+    first_seg = false;
     const int nq = ov / kGroup;
     const int u_end = (int)min((int64_t)(nq + kResidualUnits * (T - nq)), u + (x1 - x));
     const int t_beg = tile_at(u, nq), t_fin = tile_at(u_end, nq);
