@@ -733,8 +733,10 @@ __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, in
 // coherence of all XCDs without an L2 write-back), waits for them, and then
 // stores the launch's 64-bit epoch in the partial's flag.  A merge wavefront
 // reads a partial only after it has read that epoch from the flag, with
-// agent-scope loads.  Flags of earlier launches or of a fresh buffer hold
-// another value, so the workspace needs no reset.  The merge does not hold
+// agent-scope loads, and then clears the flag.  Every flag is therefore zero
+// when a launch starts -- also when a replayed graph repeats the epoch --
+// except in a fresh buffer, whose contents match a 64-bit epoch with
+// probability 2^-64; the workspace needs no reset.  The merge does not hold
 // anything a stream wavefront waits for, and there are at most half as many
 // merge workgroups as stream slots, so the stream wavefronts always run; a
 // merge wavefront that still waits after kMergeTimeoutTicks (s_memrealtime,
@@ -865,6 +867,7 @@ __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) 
         todo &= ~ready;
         while (ready) {
           int64_t slot[U];
+          uint64_t consumed = ready;  // after the loop below: the bits this round takes
 #pragma unroll
           for (int u = 0; u < U; ++u) {
             slot[u] = -1;
@@ -873,6 +876,7 @@ __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) 
               ready &= ready - 1;
             }
           }
+          consumed &= ~ready;
           uint64_t ml[U][K];
           floatx4 vv[U][K];
 #pragma unroll
@@ -894,6 +898,11 @@ __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) 
 #pragma unroll
             for (int k = 0; k < K; ++k) keep(vv[u][k]);
           }
+          // read: clear the flags, so the next launch starts from zero even
+          // when it carries the same epoch (a replayed graph does)
+          if (consumed & bit)
+            __hip_atomic_store(a.ws_flag + seg + wl, 0ull, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
           for (int u = 0; u < U; ++u) {
 #pragma unroll

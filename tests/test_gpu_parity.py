@@ -350,3 +350,37 @@ def test_caller_workspace_needs_no_initial_contents(kivi):
 def ctypes_geo(kivi, geo):
     import ctypes
     return ctypes.byref(geo.c())
+
+
+def test_decode_graph_replays_match_eager(kivi):
+    """The decode captured in a HIP graph replays with one frozen launch epoch;
+    every replay (new queries copied in, eager kernels in between) must equal
+    the eager decode bit for bit -- the merge clears each flag it consumes, so
+    a replay never sees the previous replay's partials as its own."""
+    w = wl.WORKLOADS["qwen14b"]
+    st = State(w, lens=[3000, 700, 5001, 129, 4096, 2047], seed=23)
+    st.build_oracle()
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, st.max_pages,
+                            st.num_pages)
+    cache = kivi.PagedKiviCache.from_tensors(geo, to_torch(st))
+    lens = torch.from_numpy(st.lens.astype(np.int32)).cuda()
+    bt = torch.from_numpy(st.tables).cuda()
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    qs = [torch.randn((st.batch, w.nh, w.hd), generator=gen, device="cuda").half()
+          for _ in range(4)]
+    nbytes = kivi.lib().jacq_kivi_decode_workspace_size(ctypes_geo(kivi, geo), st.batch)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    q_in = qs[0].clone()
+    out = torch.empty((st.batch, w.nh, w.hd), dtype=torch.float32, device="cuda")
+    cache.decode(q_in, lens, bt, out=out, workspace=ws)  # device set-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cache.decode(q_in, lens, bt, out=out, workspace=ws)
+    for i, q in enumerate(qs * 2):
+        q_in.copy_(q)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = cache.decode(q, lens, bt)  # eager, the library's own workspace
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), f"replay {i}"
