@@ -384,3 +384,21 @@ def test_decode_graph_replays_match_eager(kivi):
         ref = cache.decode(q, lens, bt)  # eager, the library's own workspace
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), f"replay {i}"
+
+
+def test_valu_decode_matches_oracle(kivi):
+    """The VALU split-K decode (JACQ_KIVI_DECODE=simple, a cross-check of the
+    matrix-core kernel) against the oracle, in a child process because the
+    library reads the switch once when it loads."""
+    import json
+    import os
+    import subprocess
+    import sys
+    env = dict(os.environ, JACQ_KIVI_DECODE="simple")
+    here = os.path.dirname(os.path.abspath(__file__))
+    r = subprocess.run([sys.executable, os.path.join(here, "simple_decode_check.py")], env=env,
+                       capture_output=True, text=True, timeout=100)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    worst = json.loads(r.stdout.strip().splitlines()[-1])
+    for name, excess in worst.items():
+        assert excess <= 0.0, f"{name}: worst excess over the tolerance {excess:.3e}"
