@@ -18,9 +18,13 @@
  *     sequence they compute exactly what the v1 symbols compute.
  *
  * Conventions (both groups):
- *  - every pointer is caller-owned device memory; the v1 symbols never
- *    allocate; the jacq_kivi_* symbols allocate only the split-K workspace,
- *    once per device, when the caller passes none;
+ *  - every pointer is caller-owned device memory.  The only allocation is
+ *    the library's per-device split-K workspace of the decodes: the v1 decode
+ *    symbols always use it, the jacq_kivi_* decodes when the caller passes
+ *    none.  It is allocated on first use for at least 256 sequences and
+ *    grown when a larger batch needs it, so a graph capture of a decode
+ *    allocates nothing once a call of at least its batch (or of at most 256
+ *    sequences) has run outside the capture.  The writers never allocate;
  *  - every call is asynchronous on `stream`; a cache write followed by a
  *    decode on the same stream is ordered;
  *  - fp16 tensors are IEEE binary16 bit patterns (jacq_half_t), bit

@@ -7,6 +7,7 @@
 // status code; jacq_kivi_last_error() holds the message.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdio>
 #include <cstdlib>
@@ -103,6 +104,10 @@ int current_device(int* dev) {
   }
   return JACQ_KIVI_OK;
 }
+
+// Sequences the library's own split-K workspace covers from its first use
+// (about 13 MB at the v1 geometry).
+constexpr int kLibraryWorkspaceBatch = 256;
 
 int library_workspace(int dev, size_t bytes, void** out) {
   std::lock_guard<std::mutex> lk(g_mu);
@@ -245,7 +250,12 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
   const size_t need = workspace_bytes(g, batch, sp, waves);
   if (need > 0) {
     if (ws == nullptr) {
-      if (int e = library_workspace(dev, need, &ws)) return e;
+      // sized for at least kLibraryWorkspaceBatch sequences on first use, so
+      // that later calls up to that batch (graph captures included) do not
+      // allocate
+      const size_t want =
+          std::max(need, workspace_bytes(g, std::max(batch, kLibraryWorkspaceBatch), sp, waves));
+      if (int e = library_workspace(dev, want, &ws)) return e;
     } else if (ws_bytes < need) {
       return fail(JACQ_KIVI_ENOMEM, "workspace of " + std::to_string(ws_bytes) +
                                          " bytes is smaller than the " + std::to_string(need) +
