@@ -1,9 +1,11 @@
 // kivi_writer.hip -- KIVI cache writer for gfx950.
 //
-// One workgroup per (kv head, sequence) performs the whole write in a single
-// launch: append the new fp16 tokens to the residual scratch, quantise every
-// 32-token group that ages out (K per channel over the group's tokens, V per
-// token over 32-channel groups), and shift the scratch.  The reference does
+// One workgroup per (kv head, sequence, K or V) performs that array's whole
+// write in a single launch: append the new fp16 tokens to the residual
+// scratch, quantise every 32-token group that ages out (K per channel over
+// the group's tokens, V per token over 32-channel groups), and shift the
+// scratch.  K and V share nothing, so splitting them halves the latency of the
+// workgroups that age a group out, which set the launch's time.  The reference does
 // the same in up to four launches, two of them with one thread per block
 // (integrations/vllm_kivi/source_patch.py:1532-1697, batched :1705-1775).
 //
@@ -44,13 +46,12 @@ __device__ inline float min_keep(float cur, float x) { return x < cur ? x : cur;
 __device__ inline float max_keep(float cur, float x) { return x > cur ? x : cur; }
 
 __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(2))) void kivi_append_kernel(KiviGeo g, AppendArgs a) {
-  __shared__ w4 k_tile[kGroup * 128 / 8];  // 32 tokens x HD fp16, HD <= 128
-  __shared__ w4 v_tile[kGroup * 128 / 8];
-  __shared__ w4 k_code_tile[kGroup * 64 / 16];  // 32 tokens x HD/2 code bytes
-  __shared__ w4 v_code_tile[kGroup * 64 / 16];
+  __shared__ w4 x_tile[kGroup * 128 / 8];       // 32 tokens x HD fp16, HD <= 128
+  __shared__ w4 x_code_tile[kGroup * 64 / 16];  // 32 tokens x HD/2 code bytes
 
   const int h = blockIdx.x;
   const int b = blockIdx.y;
+  const bool is_v = blockIdx.z != 0;  // this workgroup writes V (else K)
   const int tid = threadIdx.x;
   const int HD = g.hd;
   const int VPR = HD / 8;  // 16-byte vectors per fp16 row
@@ -70,47 +71,37 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
   const int D = old1 - old0;
   const bool in_scratch = (r0 + n <= g.rs);
 
-  uint16_t* ks = a.k_scr + (int64_t)b * a.scr_stride + (int64_t)h * g.rs * HD;
-  uint16_t* vs = a.v_scr + (int64_t)b * a.scr_stride + (int64_t)h * g.rs * HD;
+  uint16_t* xs = (is_v ? a.v_scr : a.k_scr) + (int64_t)b * a.scr_stride + (int64_t)h * g.rs * HD;
   const int64_t tok_stride = (int64_t)g.nkv * HD;
-  const uint16_t* nk = a.new_k + (int64_t)b * a.new_stride + (int64_t)h * HD;
-  const uint16_t* nv = a.new_v + (int64_t)b * a.new_stride + (int64_t)h * HD;
+  const uint16_t* nx = (is_v ? a.new_v : a.new_k) + (int64_t)b * a.new_stride + (int64_t)h * HD;
   const int32_t* bt = a.block_tables + (int64_t)b * a.bt_stride;
 
   // Row p of the concatenated stream [scratch rows 0..r0) ++ [new tokens].
   // Appended rows are always read from NEW_K / NEW_V, so nothing below reads
   // what this kernel writes to the scratch.
-  auto krow = [&](int p) -> const uint16_t* {
-    if (p < r0) return ks + (int64_t)p * HD;
-    return nk + (int64_t)(p - r0) * tok_stride;
-  };
-  auto vrow = [&](int p) -> const uint16_t* {
-    if (p < r0) return vs + (int64_t)p * HD;
-    return nv + (int64_t)(p - r0) * tok_stride;
+  auto xrow = [&](int p) -> const uint16_t* {
+    if (p < r0) return xs + (int64_t)p * HD;
+    return nx + (int64_t)(p - r0) * tok_stride;
   };
 
   // The first aged group's 32 rows go to LDS (the stores below cannot touch
   // them: phase 1 writes rows >= r0, the shift only after its barrier).  All
   // of a thread's loads are issued before its LDS stores: one memory latency.
   constexpr int kTilePer = kGroup * 128 / 8 / kWriterThreads;  // w4 per thread, HD <= 128
-  w4 tk[kTilePer], tv[kTilePer];
+  w4 tx[kTilePer];
   auto load_tile = [&](int gi) {
 #pragma unroll
     for (int j = 0; j < kTilePer; ++j) {
       const int i = min(tid + j * kWriterThreads, kGroup * VPR - 1);
       const int t = i / VPR, c = i % VPR;
-      tk[j] = *(const w4*)(krow(gi * kGroup + t) + c * 8);
-      tv[j] = *(const w4*)(vrow(gi * kGroup + t) + c * 8);
+      tx[j] = *(const w4*)(xrow(gi * kGroup + t) + c * 8);
     }
   };
   auto store_tile = [&]() {
 #pragma unroll
     for (int j = 0; j < kTilePer; ++j) {
       const int i = tid + j * kWriterThreads;
-      if (i < kGroup * VPR) {
-        k_tile[i] = tk[j];
-        v_tile[i] = tv[j];
-      }
+      if (i < kGroup * VPR) x_tile[i] = tx[j];
     }
   };
   // Physical pages of an aged group (first_page, first_page + 1 at page 16),
@@ -137,7 +128,7 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
   constexpr int kShiftRows = 128;
   constexpr int kPer = kShiftRows * 16 / kWriterThreads;  // w4 per thread per array, HD <= 128
   const bool shift = !(in_scratch && D == 0);
-  w4 shk[kPer], shv[kPer];
+  w4 shx[kPer];
   const int rows0 = shift ? min(kShiftRows, r1) : 0;
   // every load unconditional (a lane past the last row re-reads the last
   // row): under a per-lane branch the compiler waited for each load before
@@ -147,8 +138,7 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
     for (int j = 0; j < kPer; ++j) {
       const int i = min(tid + j * kWriterThreads, rows0 * VPR - 1);
       const int r = i / VPR, c = i % VPR;
-      shk[j] = *(const w4*)(krow(D + r) + c * 8);
-      shv[j] = *(const w4*)(vrow(D + r) + c * 8);
+      shx[j] = *(const w4*)(xrow(D + r) + c * 8);
     }
   }
 
@@ -168,19 +158,18 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
     const int keep_from = D > 0 ? max(r0, r1) : r0;
     for (int i = tid; i < (r0 + n - keep_from) * VPR; i += kWriterThreads) {
       const int r = keep_from + i / VPR, c = i % VPR;
-      *(w4*)(ks + (int64_t)r * HD + c * 8) = *(const w4*)(krow(r) + c * 8);
-      *(w4*)(vs + (int64_t)r * HD + c * 8) = *(const w4*)(vrow(r) + c * 8);
+      *(w4*)(xs + (int64_t)r * HD + c * 8) = *(const w4*)(xrow(r) + c * 8);
     }
   }
 
   // Phase 2: quantise each aged group (pack_key/pack_value_age_out_page_kernel).
-  // Every thread works: K uses four threads per channel pair (8 tokens each),
-  // V two threads per (token, 32-channel group) (16 channels each); the
+  // Every thread works: a K workgroup uses four threads per channel pair (8
+  // tokens each), a V workgroup two per (token, 32-channel group) (16
+  // channels each); the
   // partial min / max are merged in index order with the same compare-select
   // as one running loop, so ties resolve to the same (earliest) value.  Codes
   // are packed into LDS and stored as whole 16-byte row pieces.
-  uint8_t* const kcode_tile = (uint8_t*)k_code_tile;
-  uint8_t* const vcode_tile = (uint8_t*)v_code_tile;
+  uint8_t* const code_tile = (uint8_t*)x_code_tile;
   for (int gi = 0; gi < D / kGroup; ++gi) {
     const int lg = old0 / kGroup + gi;
     const int first_page = lg * ppg;
@@ -192,9 +181,9 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
     }
     const bool table_ok = first_page + ppg <= g.max_pages;
     auto phys_of = [&](int k) { return k == 0 ? gp0 : gp1; };  // page k of the group
-    const uint16_t* kt = (const uint16_t*)k_tile;
-    const uint16_t* vt = (const uint16_t*)v_tile;
-    if (tid < 2 * HD) {
+    const uint16_t* kt = (const uint16_t*)x_tile;
+    const uint16_t* vt = (const uint16_t*)x_tile;
+    if (!is_v && tid < 2 * HD) {
       // K: channel pair p = tid / 4 (channels 2p, 2p + 1), tokens 8q..8q+7.
       const int pr = tid >> 2, q = tid & 3, d0 = 2 * pr, t0 = 8 * q;
       float mn0 = h2f(kt[t0 * HD + d0]), mx0 = mn0;
@@ -236,10 +225,10 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
       for (int t = t0; t < t0 + 8; ++t) {
         const int c0 = clamp_code((h2f(kt[t * HD + d0]) - mn0) / s0);
         const int c1 = clamp_code((h2f(kt[t * HD + d0 + 1]) - mn1) / s1);
-        kcode_tile[t * HDP + pr] = (uint8_t)((c0 & 0x0f) | ((c1 & 0x0f) << 4));
+        code_tile[t * HDP + pr] = (uint8_t)((c0 & 0x0f) | ((c1 & 0x0f) << 4));
       }
     }
-    if (tid < 2 * kGroup * HDG) {
+    if (is_v && tid < 2 * kGroup * HDG) {
       // V: (token t, channel group cg) = tid / 2, channels 16 * (tid % 2) .. + 15.
       const int pr = tid >> 1, hf = tid & 1;
       const int t = pr / HDG, cg = pr % HDG;
@@ -267,7 +256,7 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
         }
         packed[w] = word;
       }
-      *(w2*)(vcode_tile + t * HDP + cg * (kGroup / 2) + 8 * hf) = w2{packed[0], packed[1]};
+      *(w2*)(code_tile + t * HDP + cg * (kGroup / 2) + 8 * hf) = w2{packed[0], packed[1]};
       if (hf == 0 && table_ok) {
         const int phys = phys_of(t / P);
         if (phys >= 0 && phys < g.num_pages) {
@@ -278,16 +267,16 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
       }
     }
     lds_barrier();
-    // packed codes: 32 rows of HD/2 bytes each for K and V, 16 bytes per thread
+    // packed codes: 32 rows of HD/2 bytes, 16 bytes per thread
     if (table_ok) {
       const int RPC = HDP / 16;  // 16-byte pieces per code row
-      for (int i = tid; i < 2 * kGroup * RPC; i += kWriterThreads) {
-        const int kv = i / (kGroup * RPC), r = (i / RPC) % kGroup, c = i % RPC;
+      for (int i = tid; i < kGroup * RPC; i += kWriterThreads) {
+        const int r = i / RPC, c = i % RPC;
         const int phys = phys_of(r / P);
         if (phys < 0 || phys >= g.num_pages) continue;
-        uint8_t* dst = (kv ? a.v_code : a.k_code) +
+        uint8_t* dst = (is_v ? a.v_code : a.k_code) +
                        (((int64_t)phys * g.nkv + h) * P + (r % P)) * HDP + 16 * c;
-        *(w4*)dst = *(const w4*)((kv ? vcode_tile : kcode_tile) + r * HDP + 16 * c);
+        *(w4*)dst = *(const w4*)(code_tile + r * HDP + 16 * c);
       }
     }
     lds_barrier();  // the tiles are rewritten by the next group
@@ -308,8 +297,7 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
         const int i = tid + j * kWriterThreads;
         if (i < rows * VPR) {
           const int r = r_base + i / VPR, c = i % VPR;
-          shk[j] = *(const w4*)(krow(D + r) + c * 8);
-          shv[j] = *(const w4*)(vrow(D + r) + c * 8);
+          shx[j] = *(const w4*)(xrow(D + r) + c * 8);
         }
       }
       __syncthreads();  // this pass's loads, in every thread, before its stores
@@ -324,16 +312,15 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
       const int i = tid + j * kWriterThreads;
       if (i < rows * VPR) {
         const int r = r_base + i / VPR, c = i % VPR;
-        *(w4*)(ks + (int64_t)r * HD + c * 8) = shk[j];
-        *(w4*)(vs + (int64_t)r * HD + c * 8) = shv[j];
+        *(w4*)(xs + (int64_t)r * HD + c * 8) = shx[j];
       }
     }
   }
 }
 
 hipError_t launch_append(const KiviGeo& g, const AppendArgs& a, int batch, hipStream_t stream) {
-  hipLaunchKernelGGL(kivi_append_kernel, dim3(g.nkv, batch), dim3(kWriterThreads), 0, stream, g,
-                     a);
+  hipLaunchKernelGGL(kivi_append_kernel, dim3(g.nkv, batch, 2), dim3(kWriterThreads), 0, stream,
+                     g, a);
   return hipGetLastError();
 }
 
