@@ -402,3 +402,24 @@ def test_valu_decode_matches_oracle(kivi):
     worst = json.loads(r.stdout.strip().splitlines()[-1])
     for name, excess in worst.items():
         assert excess <= 0.0, f"{name}: worst excess over the tolerance {excess:.3e}"
+
+
+def test_caller_workspace_too_small_is_rejected(kivi):
+    """A caller workspace one byte short of jacq_kivi_decode_workspace_size is
+    refused before anything is launched (status JACQ_KIVI_ENOMEM, message
+    naming both sizes), and the output is left untouched."""
+    w = wl.WORKLOADS["qwen14b"]
+    st = State(w, lens=[700, 300], seed=2)
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, st.max_pages,
+                            st.num_pages)
+    cache = kivi.PagedKiviCache.from_tensors(geo, to_torch(st))
+    nbytes = kivi.lib().jacq_kivi_decode_workspace_size(ctypes_geo(kivi, geo), st.batch)
+    assert nbytes > 0
+    ws = torch.zeros(nbytes - 1, dtype=torch.uint8, device="cuda")
+    out = torch.full((st.batch, w.nh, w.hd), 7.0, dtype=torch.float32, device="cuda")
+    with pytest.raises(kivi.KiviLaunchError, match=f"smaller than the {nbytes} required"):
+        cache.decode(torch.from_numpy(st.q).view(torch.float16).cuda(),
+                     torch.from_numpy(st.lens.astype(np.int32)).cuda(),
+                     torch.from_numpy(st.tables).cuda(), out=out, workspace=ws)
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
