@@ -423,3 +423,19 @@ def test_caller_workspace_too_small_is_rejected(kivi):
                      torch.from_numpy(st.tables).cuda(), out=out, workspace=ws)
     torch.cuda.synchronize()
     assert bool((out == 7.0).all())
+
+
+@pytest.mark.parametrize("nh,nkv,hd,page,lens", [
+    (32, 2, 128, 16, [3000, 129, 700]),   # G = 16: the unpacked HD=128 kernel
+    (36, 4, 128, 32, [1500, 161]),        # G = 9, page 32
+    (24, 2, 64, 32, [2048, 33, 1]),       # G = 12, HD = 64
+    (18, 2, 64, 16, [900, 4000]),         # G = 9, HD = 64, page 16
+    (8, 8, 128, 16, [1200, 77]),          # G = 1 (multi-head attention)
+], ids=["g16_hd128_p16", "g9_hd128_p32", "g12_hd64_p32", "g9_hd64_p16", "g1_hd128_p16"])
+def test_decode_other_gqa_ratios(kivi, nh, nkv, hd, page, lens):
+    """GQA ratios outside the benchmark configs: G > 8 runs the unpacked kernels
+    (one query head per MFMA column), G = 1 the packed one with a single head."""
+    w = wl.Workload(f"g{nh // nkv}", nh, nkv, hd, len(lens), min(lens), max(lens), page=page,
+                    residual=128, outliers=4, outlier_scale=8.0, seed=31)
+    st, out = _decode_case(kivi, w, lens, seed=31)
+    assert_close(out, st.decode_ref(), f"decode G={nh // nkv} HD={hd} page={page}")
