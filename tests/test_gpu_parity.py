@@ -439,3 +439,44 @@ def test_decode_other_gqa_ratios(kivi, nh, nkv, hd, page, lens):
                     residual=128, outliers=4, outlier_scale=8.0, seed=31)
     st, out = _decode_case(kivi, w, lens, seed=31)
     assert_close(out, st.decode_ref(), f"decode G={nh // nkv} HD={hd} page={page}")
+
+
+@pytest.mark.parametrize("residual", [64, 256])
+def test_other_residual_windows_write_and_decode(kivi, residual):
+    """Residual windows other than 32 / 128 (any multiple of 32 is accepted):
+    a bulk prefill, then one-token steps crossing age-out boundaries; pool and
+    scratch bit-exact, decode within tolerance.  R = 256 makes the scratch
+    shift run three 128-row passes."""
+    w = wl.WORKLOADS["mistral7b"].scaled(batch=3, ctx_lo=600, residual=residual)
+    lens = np.array([600, residual + 31, 1000])
+    st = State(w, lens=lens, extra_tokens=40, seed=41)
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, st.max_pages,
+                            st.num_pages)
+    cache = kivi.PagedKiviCache(geo, st.batch)
+    bt = torch.from_numpy(st.tables).cuda()
+    hist_k = [torch.from_numpy(k).view(torch.float16).cuda() for k in st.k_hist]
+    hist_v = [torch.from_numpy(v).view(torch.float16).cuda() for v in st.v_hist]
+    for b in range(st.batch):
+        L = int(lens[b])
+        cache.sequence_view(b).append(hist_k[b][None, :L].contiguous(),
+                                      hist_v[b][None, :L].contiguous(), bt[b:b + 1].contiguous(),
+                                      torch.zeros(1, dtype=torch.int32, device="cuda"))
+    st.build_oracle()
+    cur = lens.copy()
+    for _ in range(40):
+        nk = torch.stack([hist_k[b][cur[b]] for b in range(st.batch)])[:, None].contiguous()
+        nv = torch.stack([hist_v[b][cur[b]] for b in range(st.batch)])[:, None].contiguous()
+        cache.append(nk, nv, bt, torch.from_numpy(cur.astype(np.int32)).cuda())
+        for b in range(st.batch):
+            o.cache_write(st.cache, b, st.k_hist[b][cur[b]], st.v_hist[b][cur[b]], st.tables[b],
+                          int(cur[b]) + 1)
+        cur += 1
+    torch.cuda.synchronize()
+    g = dict(zip(("k_code", "k_scale", "k_zero", "v_code", "v_scale", "v_zero", "k_scr", "v_scr"),
+                 cache.pool()))
+    res = [int(n - wl.split_old_tokens(int(n), w.residual)) for n in cur]
+    _compare_pool(st, g, scratch_rows=res, what=f"R={residual}")
+    q = torch.from_numpy(st.q).view(torch.float16).cuda()
+    out = cache.decode(q, torch.from_numpy(cur.astype(np.int32)).cuda(), bt)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), st.decode_ref(cur), f"decode R={residual}")
