@@ -68,7 +68,7 @@ def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the decode path shards by sequence or kv head with no exchange; see DESIGN.md)",
+              "(the decode path shards by sequence or kv head, with no exchange inside attention)",
               file=sys.stderr)
         return 2
 
