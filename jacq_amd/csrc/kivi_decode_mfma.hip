@@ -37,6 +37,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 #include <type_traits>
 #include <utility>
 
@@ -743,6 +744,18 @@ __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, in
 // 100 MHz) writes NaN for its segments and ends, so the launch always drains.
 constexpr uint64_t kMergeTimeoutTicks = 100000000;  // 1 s
 
+// Test-only: JACQ_KIVI_TEST_MERGE_TIMEOUT_US=<us>, read once, makes every
+// merge wait for an epoch no stream wave stores and give up after <us>, so a
+// test can check from the host that a launch whose merges time out still
+// drains (whole segments correct, merged ones NaN).  Unset in normal use.
+static uint64_t test_merge_timeout_ticks() {
+  static const uint64_t t = [] {
+    const char* e = std::getenv("JACQ_KIVI_TEST_MERGE_TIMEOUT_US");
+    return e ? (uint64_t)std::strtoull(e, nullptr, 10) * 100 : 0;  // 100 MHz ticks
+  }();
+  return t;
+}
+
 // Global unit index of (b, kv head 0): NKV times the units of the sequences before b.
 __device__ inline int64_t seq_start(const KiviGeo& g, const DecodeArgs& a, int b, int lane) {
   int64_t run = 0;
@@ -800,7 +813,7 @@ __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) 
   const int64_t TT = stream_units(g, a, lane);
   const int64_t W = stream_waves(TT, a.waves);
   const int nseg = a.batch * NKV;
-  const uint64_t epoch = a.epoch, t_start = __builtin_amdgcn_s_memrealtime();
+  const uint64_t epoch = a.epoch + a.merge_skew, t_start = __builtin_amdgcn_s_memrealtime();
   bool late = false;  // wave-uniform: the wait ran out
   int gi[K], d[K];
   bool on[K];
@@ -851,7 +864,7 @@ __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) 
         // one lane waits for the first piece in order ...
         if (lane == __builtin_ctzll(todo)) {
           while (ld_agent(flag) != epoch &&
-                 __builtin_amdgcn_s_memrealtime() - t_start <= kMergeTimeoutTicks)
+                 __builtin_amdgcn_s_memrealtime() - t_start <= a.merge_timeout)
             __builtin_amdgcn_s_sleep(4);
         }
         // ... then one round finds how many after it have landed too
@@ -1237,6 +1250,12 @@ hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& args, int batc
   DecodeArgs a = args;
   a.epoch = epochs.fetch_add(1, std::memory_order_relaxed) + 1;
   a.merge_wgs = std::max(1, std::min(batch * g.nkv, a.waves / 2));
+  a.merge_timeout = kMergeTimeoutTicks;
+  a.merge_skew = 0;
+  if (const uint64_t t = test_merge_timeout_ticks()) {
+    a.merge_timeout = t;
+    a.merge_skew = 1;
+  }
   // Profiling only.  With main_end, the kernel's start and end are stamped by
   // the command processor (its own duration, as a kernel trace reads it);
   // that launch form delays the next kernel by a few microseconds, so without

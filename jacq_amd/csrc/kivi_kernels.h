@@ -51,6 +51,8 @@ struct DecodeArgs {
   int waves;       // matrix-core kernel: wavefronts sharing the tile stream
   int merge_wgs = 0;       // matrix-core kernel: merge workgroups after the stream wavefronts
   uint64_t epoch = 0;      // matrix-core kernel: this launch's tag (set by the launcher)
+  uint64_t merge_timeout = 0;  // matrix-core kernel: s_memrealtime ticks a merge waits at most
+  uint64_t merge_skew = 0;     // matrix-core kernel: 0; 1 only in the forced-timeout test
   int retained_pages = -1;  // >= 0: sparse-retained window (compact block table)
 };
 

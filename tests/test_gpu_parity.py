@@ -480,3 +480,22 @@ def test_other_residual_windows_write_and_decode(kivi, residual):
     out = cache.decode(q, torch.from_numpy(cur.astype(np.int32)).cuda(), bt)
     torch.cuda.synchronize()
     assert_close(out.cpu().numpy(), st.decode_ref(cur), f"decode R={residual}")
+
+
+def test_merge_timeout_drains(kivi):
+    """Failure handling of the in-launch merge, forced from the host: with
+    JACQ_KIVI_TEST_MERGE_TIMEOUT_US the merge waits for an epoch nobody stores
+    and gives up after 20 us.  The launch still ends; segments a single
+    wavefront wrote whole stay correct and every merged segment is NaN."""
+    import json
+    import os
+    import subprocess
+    import sys
+    env = dict(os.environ, JACQ_KIVI_TEST_MERGE_TIMEOUT_US="20")
+    here = os.path.dirname(os.path.abspath(__file__))
+    r = subprocess.run([sys.executable, os.path.join(here, "merge_timeout_check.py")], env=env,
+                       capture_output=True, text=True, timeout=100)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    counts = json.loads(r.stdout.strip().splitlines()[-1])
+    assert counts["other"] == 0, counts
+    assert counts["nan"] >= 1, counts
