@@ -180,3 +180,17 @@ def test_gpu_written_cache_round_trips_and_decodes_identically(tmp_path):
     got = c2.decode(q, sl2, bt2)
     torch.cuda.synchronize()
     assert torch.equal(ref.view(torch.int32), got.view(torch.int32))
+
+
+@pytest.mark.parametrize("residual,max_pages", [(128, 124), (32, 40)])
+def test_old_valid_is_the_decode_window(residual, max_pages):
+    """cache_io.old_valid (which pages a compact dump keeps) against the
+    oracle's split rule on the clamped length, for every length from 0 to past
+    the clamp: whole groups, never more than the length allows, at most LQ."""
+    geo = kivi.KiviGeometry(40, 8, 128, 16, 32, residual, max_pages, 1)
+    lq = max_pages * 16 // 32 * 32
+    for n in range(0, lq + residual + 100):
+        ov = cache_io.old_valid(geo, n)
+        ref = min(o.split_old_tokens(min(n, lq + residual), residual, 32), lq)
+        assert ov == ref, n
+        assert ov % 32 == 0 and 0 <= ov <= max(0, min(n, lq + residual) - residual)
