@@ -9,8 +9,8 @@
 // the same in up to four launches, two of them with one thread per block
 // (integrations/vllm_kivi/source_patch.py:1532-1697, batched :1705-1775).
 //
-// Arithmetic is kept bit-exact with the reference: fp32 min/max over fp16
-// inputs in token (K) or channel (V) order, scale = (max - min) / 15 with
+// Arithmetic is kept bit-exact with the reference: fp32 fminf/fmaxf over fp16
+// inputs, scale = (max - min) / 15 with
 // IEEE division, scale <= 0 -> 1, codes = clamp(rint((x - min) / scale)),
 // scale and min stored as fp16 with round-to-nearest-even.
 #include "kivi_kernels.h"
@@ -27,11 +27,16 @@ typedef uint32_t w2 __attribute__((ext_vector_type(2)));
 
 #pragma clang fp contract(off)
 
-__device__ inline int clamp_code(float x) {  // source_patch.py:1517-1522
-  const int code = (int)__builtin_rintf(x);
-  if (code < 0) return 0;
-  if (code > 15) return 15;
-  return code;
+// static_cast<int>(rintf(x)) clamped to [0, 15] (source_patch.py:1517-1522),
+// with the conversion CUDA and gfx950 hardware perform: out-of-range values
+// saturate, NaN becomes 0.  Clamped in the float domain, because an
+// out-of-range float -> int conversion is undefined in C++ and the compiler
+// may assume it does not happen.
+__device__ inline int clamp_code(float x) {
+  const float r = __builtin_rintf(x);
+  if (r >= 15.0f) return 15;
+  if (r >= 0.0f) return (int)r;
+  return 0;  // negative or NaN
 }
 
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
@@ -41,9 +46,24 @@ __device__ inline void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Compare-and-select running min/max: ties (+0 / -0) keep the earlier value.
-__device__ inline float min_keep(float cur, float x) { return x < cur ? x : cur; }
-__device__ inline float max_keep(float cur, float x) { return x > cur ? x : cur; }
+// fminf / fmaxf of the reference's age-out kernels (source_patch.py:1555-1558,
+// :1598-1599): a NaN operand is dropped, NaN results only when both are NaN.
+// For a +0 / -0 pair, min gives -0 and max +0 (C Annex F's recommendation;
+// LLVM's minnum leaves it open, so it is written out).  Both are then
+// commutative and associative: the partial reductions below may merge in any
+// order and still give one sequential loop's bits.
+__device__ inline float min_num(float a, float b) {
+  if (b != b) return a;
+  if (a != a) return b;
+  if (a == b) return __uint_as_float(__float_as_uint(a) | __float_as_uint(b));
+  return b < a ? b : a;
+}
+__device__ inline float max_num(float a, float b) {
+  if (b != b) return a;
+  if (a != a) return b;
+  if (a == b) return __uint_as_float(__float_as_uint(a) & __float_as_uint(b));
+  return b > a ? b : a;
+}
 
 __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(2))) void kivi_append_kernel(KiviGeo g, AppendArgs a) {
   __shared__ w4 x_tile[kGroup * 128 / 8];       // 32 tokens x HD fp16, HD <= 128
@@ -165,10 +185,8 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
   // Phase 2: quantise each aged group (pack_key/pack_value_age_out_page_kernel).
   // Every thread works: a K workgroup uses four threads per channel pair (8
   // tokens each), a V workgroup two per (token, 32-channel group) (16
-  // channels each); the
-  // partial min / max are merged in index order with the same compare-select
-  // as one running loop, so ties resolve to the same (earliest) value.  Codes
-  // are packed into LDS and stored as whole 16-byte row pieces.
+  // channels each); the partial min / max merge through shuffles, in any
+  // order since min_num / max_num are associative.  Codes are packed into LDS and stored as whole 16-byte row pieces.
   uint8_t* const code_tile = (uint8_t*)x_code_tile;
   for (int gi = 0; gi < D / kGroup; ++gi) {
     const int lg = old0 / kGroup + gi;
@@ -191,20 +209,17 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
       for (int t = t0 + 1; t < t0 + 8; ++t) {
         const float x0 = h2f(kt[t * HD + d0]), x1 = h2f(kt[t * HD + d0 + 1]);
-        mn0 = min_keep(mn0, x0);
-        mx0 = max_keep(mx0, x0);
-        mn1 = min_keep(mn1, x1);
-        mx1 = max_keep(mx1, x1);
+        mn0 = min_num(mn0, x0);
+        mx0 = max_num(mx0, x0);
+        mn1 = min_num(mn1, x1);
+        mx1 = max_num(mx1, x1);
       }
 #pragma unroll
-      for (int off = 1; off < 4; off <<= 1) {  // merge quarters in token order
-        const bool first = (q & off) == 0;    // this lane holds the earlier tokens
-        const float on0 = __shfl_xor(mn0, off, 64), ox0 = __shfl_xor(mx0, off, 64);
-        const float on1 = __shfl_xor(mn1, off, 64), ox1 = __shfl_xor(mx1, off, 64);
-        mn0 = first ? min_keep(mn0, on0) : min_keep(on0, mn0);
-        mx0 = first ? max_keep(mx0, ox0) : max_keep(ox0, mx0);
-        mn1 = first ? min_keep(mn1, on1) : min_keep(on1, mn1);
-        mx1 = first ? max_keep(mx1, ox1) : max_keep(ox1, mx1);
+      for (int off = 1; off < 4; off <<= 1) {  // merge the four quarters
+        mn0 = min_num(mn0, __shfl_xor(mn0, off, 64));
+        mx0 = max_num(mx0, __shfl_xor(mx0, off, 64));
+        mn1 = min_num(mn1, __shfl_xor(mn1, off, 64));
+        mx1 = max_num(mx1, __shfl_xor(mx1, off, 64));
       }
       float s0 = (mx0 - mn0) / 15.0f;
       float s1 = (mx1 - mn1) / 15.0f;
@@ -237,12 +252,11 @@ __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
       for (int c = 1; c < 16; ++c) {
         const float x = h2f(row[c]);
-        mn = min_keep(mn, x);
-        mx = max_keep(mx, x);
+        mn = min_num(mn, x);
+        mx = max_num(mx, x);
       }
-      const float on = __shfl_xor(mn, 1, 64), ox = __shfl_xor(mx, 1, 64);
-      mn = hf == 0 ? min_keep(mn, on) : min_keep(on, mn);
-      mx = hf == 0 ? max_keep(mx, ox) : max_keep(ox, mx);
+      mn = min_num(mn, __shfl_xor(mn, 1, 64));
+      mx = max_num(mx, __shfl_xor(mx, 1, 64));
       float sv = (mx - mn) / 15.0f;
       if (!(sv > 0.0f)) sv = 1.0f;
       uint32_t packed[2];

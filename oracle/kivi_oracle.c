@@ -87,18 +87,39 @@ int32_t kivi_split_old_tokens(int32_t seq_len, int32_t residual, int32_t group) 
 
 static inline int32_t scratch_rows(const kivi_geo* g) { return g->residual + g->group; }
 
-/* clamp_code, source_patch.py:1517-1522: rintf (ties to even), clamp [0,15]. */
+/* clamp_code, source_patch.py:1517-1522: static_cast<int>(rintf(x)) clamped
+ * to [0, 15].  rintf rounds ties to even.  The float -> int conversion is
+ * CUDA's cvt.rzi.s32.f32 (and gfx950's v_cvt_i32_f32): out-of-range values
+ * saturate and NaN becomes 0.  C leaves that conversion undefined, so it is
+ * spelled out here in the float domain: NaN -> 0, +inf -> 15, -inf -> 0. */
 static inline int32_t clamp_code(float x) {
-  const int32_t code = (int32_t)rintf(x);
-  if (code < 0) return 0;
-  if (code > 15) return 15;
-  return code;
+  const float r = rintf(x);
+  if (r >= 15.0f) return 15;
+  if (r >= 0.0f) return (int32_t)r;
+  return 0; /* negative or NaN */
 }
 
-/* Running min/max, written as compare-and-select so that ties between +0 and
- * -0 keep the earlier value (the HIP kernels use the same rule). */
-static inline float min_keep(float cur, float x) { return x < cur ? x : cur; }
-static inline float max_keep(float cur, float x) { return x > cur ? x : cur; }
+/* fminf / fmaxf, source_patch.py:1555-1558 (K) and :1598-1599 (V).  A NaN
+ * operand is dropped (the other one is returned; NaN only when both are).
+ * The sign of a zero result is not fixed by fminf's contract; C's Annex F
+ * (F.10.9.2) recommends min(-0, +0) = -0 and max(-0, +0) = +0, which makes
+ * both operations commutative and associative, so a reduction in any order
+ * gives the same bits.  Equal nonzero operands have equal bits, so the OR /
+ * AND below only matters for a +0 / -0 pair. */
+static inline uint32_t f32_bits(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
+static inline float bits_f32(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
+static inline float min_num(float a, float b) {
+  if (b != b) return a;
+  if (a != a) return b;
+  if (a == b) return bits_f32(f32_bits(a) | f32_bits(b));
+  return b < a ? b : a;
+}
+static inline float max_num(float a, float b) {
+  if (b != b) return a;
+  if (a != a) return b;
+  if (a == b) return bits_f32(f32_bits(a) & f32_bits(b));
+  return b > a ? b : a;
+}
 
 /* ---- group pack: K source_patch.py:1532-1581, V :1583-1620 ---- */
 
@@ -118,8 +139,8 @@ void kivi_ref_pack_group(const kivi_geo* g, int32_t h, const uint16_t* const* k_
     float mx = mn;
     for (int32_t t = 1; t < GS; ++t) {
       const float x = kivi_f16_to_f32(k_rows[t][d]);
-      mn = min_keep(mn, x);
-      mx = max_keep(mx, x);
+      mn = min_num(mn, x);
+      mx = max_num(mx, x);
     }
     float scale = (mx - mn) / 15.0f;
     if (!(scale > 0.0f)) scale = 1.0f;
@@ -150,8 +171,8 @@ void kivi_ref_pack_group(const kivi_geo* g, int32_t h, const uint16_t* const* k_
       float mx = mn;
       for (int32_t c = 1; c < GS; ++c) {
         const float x = kivi_f16_to_f32(v_rows[t][d0 + c]);
-        mn = min_keep(mn, x);
-        mx = max_keep(mx, x);
+        mn = min_num(mn, x);
+        mx = max_num(mx, x);
       }
       float scale = (mx - mn) / 15.0f;
       if (!(scale > 0.0f)) scale = 1.0f;
