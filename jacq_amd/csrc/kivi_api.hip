@@ -81,56 +81,117 @@ KiviGeo make_geo(const jacq_kivi_geometry& x) {
   return g;
 }
 
-// ---- device properties and the library-owned split-K workspace ----
+// ---- per-device state: CU count, merge status word, library workspaces ----
 
+// A library-owned split-K workspace, one per (device, stream): decodes on
+// different streams may run at the same time and must not share partial
+// slots.  An outgrown buffer is never freed (a captured graph may still hold
+// its address); it moves to `retired` and lives until the process ends.
+struct StreamWorkspace {
+  hipStream_t stream;
+  void* ptr;
+  size_t bytes;
+};
 struct DeviceState {
   int cus = 0;
-  void* ws = nullptr;
-  size_t ws_bytes = 0;
+  // Pinned, host-coherent word the decode kernels set (system-scope vector
+  // store) when a split-K merge wait runs out; read by the host without a
+  // synchronisation, cleared by jacq_kivi_decode_status.
+  volatile uint32_t* status = nullptr;
+  uint32_t* status_dev = nullptr;  // the same word, as the device addresses it
+  std::vector<StreamWorkspace> ws;
+  std::vector<StreamWorkspace> retired;
 };
 std::mutex g_mu;
 std::vector<DeviceState> g_dev;
 
-int current_device(int* dev) {
-  if (hipGetDevice(dev) != hipSuccess) return fail(JACQ_KIVI_EHIP, "hipGetDevice failed");
-  std::lock_guard<std::mutex> lk(g_mu);
-  if ((int)g_dev.size() <= *dev) g_dev.resize(*dev + 1);
-  if (g_dev[*dev].cus == 0) {
+// Per-device set-up, once, with the device current.  Called by every entry
+// point (and by jacq_kivi_init); everything it allocates lives until exit.
+int init_device_locked(int dev) {
+  if ((int)g_dev.size() <= dev) g_dev.resize(dev + 1);
+  DeviceState& s = g_dev[dev];
+  if (s.cus == 0) {
     int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, *dev) != hipSuccess ||
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
       cus = 256;
-    g_dev[*dev].cus = cus;
+    s.cus = cus;
+  }
+  if (!s.status) {
+    void* p = nullptr;
+    if (hipHostMalloc(&p, 64, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess || !p)
+      return fail(JACQ_KIVI_ENOMEM, "hipHostMalloc of the decode status word failed");
+    void* d = nullptr;
+    if (hipHostGetDevicePointer(&d, p, 0) != hipSuccess || !d)
+      return fail(JACQ_KIVI_EHIP, "hipHostGetDevicePointer(status word) failed");
+    *(volatile uint32_t*)p = 0;
+    s.status = (volatile uint32_t*)p;
+    s.status_dev = (uint32_t*)d;
   }
   return JACQ_KIVI_OK;
 }
+
+int current_device(int* dev) {
+  if (hipGetDevice(dev) != hipSuccess) return fail(JACQ_KIVI_EHIP, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lk(g_mu);
+  return init_device_locked(*dev);
+}
+
+// Fields of a device set up by current_device (the vector may grow under
+// other threads, so every read takes the lock).
+struct DeviceInfo {
+  int cus;
+  volatile uint32_t* status;
+  uint32_t* status_dev;
+};
+DeviceInfo device_state(int dev) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const DeviceState& s = g_dev[dev];
+  return {s.cus, s.status, s.status_dev};
+}
+
+constexpr const char* kTimeoutMsg =
+    "a split-K merge of an earlier decode on this device timed out and wrote NaN "
+    "(its stream wavefronts never ran); call jacq_kivi_decode_status() to reset";
 
 // Sequences the library's own split-K workspace covers from its first use
 // (about 13 MB at the v1 geometry).
 constexpr int kLibraryWorkspaceBatch = 256;
 
-int library_workspace(int dev, size_t bytes, void** out) {
+int library_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
   std::lock_guard<std::mutex> lk(g_mu);
   DeviceState& s = g_dev[dev];
-  if (s.ws_bytes < bytes) {
-    if (s.ws) {
-      // hipFree waits for work that may still read the old buffer.
-      if (hipFree(s.ws) != hipSuccess) return fail(JACQ_KIVI_EHIP, "hipFree(workspace) failed");
-      s.ws = nullptr;
-      s.ws_bytes = 0;
-    }
+  StreamWorkspace* w = nullptr;
+  for (auto& x : s.ws)
+    if (x.stream == stream) w = &x;
+  if (!w) {
+    s.ws.push_back({stream, nullptr, 0});
+    w = &s.ws.back();
+  }
+  if (w->bytes < bytes) {
+    if (w->ptr) s.retired.push_back(*w);
+    w->ptr = nullptr;
+    w->bytes = 0;
     const size_t want = bytes + bytes / 4;
-    if (hipMalloc(&s.ws, want) != hipSuccess) {
-      s.ws = nullptr;
+    void* p = nullptr;
+    // The first decode on a stream may be inside a stream capture (a graph
+    // captured on a fresh stream); an allocation is not a stream operation,
+    // so this thread's capture mode is relaxed around it, as the runtime
+    // allows, instead of invalidating the capture.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const bool swapped = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
+    const hipError_t me = hipMalloc(&p, want);
+    if (swapped) (void)hipThreadExchangeStreamCaptureMode(&mode);
+    if (me != hipSuccess)
       return fail(JACQ_KIVI_ENOMEM, "hipMalloc of " + std::to_string(want) +
                                          " workspace bytes failed");
-    }
-    // zeroed once: no flag of a fresh buffer matches a launch epoch (they start at 1)
-    if (hipMemset(s.ws, 0, want) != hipSuccess)
-      return fail(JACQ_KIVI_EHIP, "hipMemset(workspace) failed");
-    s.ws_bytes = want;
+    // Not cleared: a flag counts only when it equals the launch's epoch (a
+    // random 64-bit value with the top bit set), and a synchronous memset
+    // could not run inside a stream capture, where this allocation may happen.
+    w->ptr = p;
+    w->bytes = want;
   }
-  *out = s.ws;
+  *out = w->ptr;
   return JACQ_KIVI_OK;
 }
 
@@ -239,6 +300,8 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
   const KiviGeo g = make_geo(x);
   int dev = 0;
   if (int e = current_device(&dev)) return e;
+  const DeviceInfo ds = device_state(dev);
+  if (*ds.status != 0) return fail(JACQ_KIVI_ETIMEOUT, kTimeoutMsg);
   int64_t max_tokens = max_seq_len(x);
   if (seq_len_host >= 0) {
     int ov, rv;
@@ -246,7 +309,7 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
     max_tokens = ov + rv;
   }
   const SplitPlan sp = plan_splits(max_tokens);
-  const int waves = jacq::decode_stream_waves(g, g_dev[dev].cus);
+  const int waves = jacq::decode_stream_waves(g, ds.cus);
   const size_t need = workspace_bytes(g, batch, sp, waves);
   if (need > 0) {
     if (ws == nullptr) {
@@ -255,7 +318,7 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
       // allocate
       const size_t want =
           std::max(need, workspace_bytes(g, std::max(batch, kLibraryWorkspaceBatch), sp, waves));
-      if (int e = library_workspace(dev, want, &ws)) return e;
+      if (int e = library_workspace(dev, stream, want, &ws)) return e;
     } else if (ws_bytes < need) {
       return fail(JACQ_KIVI_ENOMEM, "workspace of " + std::to_string(ws_bytes) +
                                          " bytes is smaller than the " + std::to_string(need) +
@@ -281,6 +344,7 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
   a.out = O;
   a.out_stride = (int64_t)g.nh * g.hd;
   a.retained_pages = retained_pages;
+  a.status = ds.status_dev;
   fill_ws(a, g, batch, sp, waves, need > 0 ? ws : nullptr);
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   profile_slot(ev);
@@ -336,12 +400,18 @@ int run_append(const jacq_kivi_geometry& x, uint8_t* kc, jacq_half_t* ksc, jacq_
   return JACQ_KIVI_OK;
 }
 
-// CUDA_CHECK of the emitted v1 symbols: report and exit(1).
+// CUDA_CHECK of the emitted v1 symbols: report and exit(1).  A merge
+// time-out of an earlier decode is reported the same way by the next v1
+// decode on the device.
 void v1_check(int status, const char* where) {
   if (status == JACQ_KIVI_OK) return;
-  const hipError_t e = hipGetLastError();
-  std::fprintf(stderr, "HIP error %s in %s: %s\n", hipGetErrorString(e), where,
-               g_last_error.c_str());
+  if (status == JACQ_KIVI_EHIP) {
+    const hipError_t e = hipGetLastError();
+    std::fprintf(stderr, "HIP error %s in %s: %s\n", hipGetErrorString(e), where,
+                 g_last_error.c_str());
+  } else {
+    std::fprintf(stderr, "jacq_kivi error %d in %s: %s\n", status, where, g_last_error.c_str());
+  }
   std::exit(1);
 }
 
@@ -354,6 +424,41 @@ int jacq_kivi_ext_version(void) { return JACQ_KIVI_EXT_VERSION; }
 const char* jacq_kivi_last_error(void) { return g_last_error.c_str(); }
 
 int jacq_kivi_check_geometry(const jacq_kivi_geometry* geo) { return check_geometry(geo); }
+
+int jacq_kivi_init(void) {
+  int dev = 0;
+  return current_device(&dev);
+}
+
+int jacq_kivi_decode_status(void* workspace, size_t workspace_bytes_, hipStream_t stream) {
+  int dev = 0;
+  if (int e = current_device(&dev)) return e;
+  if (hipStreamSynchronize(stream) != hipSuccess)
+    return fail(JACQ_KIVI_EHIP, "hipStreamSynchronize failed");
+  const DeviceInfo ds = device_state(dev);
+  if (*ds.status == 0) return JACQ_KIVI_OK;
+  // Reset: a timed-out merge left flags that its stream wavefronts set after
+  // it gave up; a graph replay (same epoch) would take them for its own.
+  // Every workspace the device's decodes may have used is cleared.
+  if (hipDeviceSynchronize() != hipSuccess) return fail(JACQ_KIVI_EHIP, "hipDeviceSynchronize failed");
+  std::vector<StreamWorkspace> all;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    all = g_dev[dev].ws;
+    all.insert(all.end(), g_dev[dev].retired.begin(), g_dev[dev].retired.end());
+  }
+  if (workspace && workspace_bytes_) all.push_back({stream, workspace, workspace_bytes_});
+  for (const auto& w : all)
+    if (w.ptr && hipMemset(w.ptr, 0, w.bytes) != hipSuccess)
+      return fail(JACQ_KIVI_EHIP, "hipMemset(workspace) failed");
+  *ds.status = 0;
+  return fail(JACQ_KIVI_ETIMEOUT, "a split-K merge timed out since the last query; its "
+                                  "outputs were NaN; the workspaces are reset");
+}
+
+void jacq_kivi_test_force_merge_timeout(uint32_t microseconds) {
+  jacq::set_test_merge_timeout_us(microseconds);
+}
 
 int64_t jacq_kivi_max_seq_len(const jacq_kivi_geometry* geo) {
   if (check_geometry(geo) != JACQ_KIVI_OK) return -1;
@@ -383,7 +488,7 @@ size_t jacq_kivi_decode_workspace_size(const jacq_kivi_geometry* geo, int32_t ba
   if (current_device(&dev) != JACQ_KIVI_OK) return 0;
   const KiviGeo g = make_geo(*geo);
   return workspace_bytes(g, batch, plan_splits(max_seq_len(*geo)),
-                         jacq::decode_stream_waves(g, g_dev[dev].cus));
+                         jacq::decode_stream_waves(g, device_state(dev).cus));
 }
 
 int jacq_kivi_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q, const int32_t* SEQ_LENS,

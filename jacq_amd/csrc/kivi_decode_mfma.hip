@@ -37,7 +37,9 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cstdlib>
+#include <random>
 #include <type_traits>
 #include <utility>
 
@@ -744,16 +746,13 @@ __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, in
 // 100 MHz) writes NaN for its segments and ends, so the launch always drains.
 constexpr uint64_t kMergeTimeoutTicks = 100000000;  // 1 s
 
-// Test-only: JACQ_KIVI_TEST_MERGE_TIMEOUT_US=<us>, read once, makes every
-// merge wait for an epoch no stream wave stores and give up after <us>, so a
-// test can check from the host that a launch whose merges time out still
-// drains (whole segments correct, merged ones NaN).  Unset in normal use.
-static uint64_t test_merge_timeout_ticks() {
-  static const uint64_t t = [] {
-    const char* e = std::getenv("JACQ_KIVI_TEST_MERGE_TIMEOUT_US");
-    return e ? (uint64_t)std::strtoull(e, nullptr, 10) * 100 : 0;  // 100 MHz ticks
-  }();
-  return t;
+// Test-only (jacq_kivi_test_force_merge_timeout): when nonzero, every merge
+// waits for an epoch no stream wave stores and gives up after this many
+// s_memrealtime ticks, so a test can check from the host that a launch whose
+// merges time out still drains and reports it.  Zero in normal use.
+static std::atomic<uint64_t> g_test_merge_timeout_ticks{0};
+void set_test_merge_timeout_us(uint32_t us) {
+  g_test_merge_timeout_ticks.store((uint64_t)us * 100, std::memory_order_relaxed);  // 100 MHz
 }
 
 // Global unit index of (b, kv head 0): NKV times the units of the sequences before b.
@@ -940,6 +939,9 @@ __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) 
         *(floatx4*)(out + (int64_t)gi[k] * HD + d[k]) =
             late ? floatx4{NAN, NAN, NAN, NAN} : acc[k] / fmaxf(Lsum[k], 1.0e-30f);
   }
+  // a wait ran out: the host sees it in the device's status word
+  if (late && lane == 0 && a.status)
+    __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 template <int HD, int P, bool PACK>
@@ -1246,13 +1248,21 @@ hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& args, int batc
   // One launch: the stream wavefronts, then the merge workgroups (at most
   // half as many as stream slots, each taking segments in turn).  Every
   // launch gets its own epoch, which marks the partials it stores.
-  static std::atomic<uint64_t> epochs{0};
+  // Epochs start from a random 64-bit value with the top bit set, so that
+  // leftover workspace contents (zeros, small integers, earlier epochs of
+  // other processes) are unlikely to match one.
+  static std::atomic<uint64_t> epochs{[] {
+    std::random_device rd;
+    const uint64_t t = (uint64_t)std::chrono::steady_clock::now().time_since_epoch().count();
+    const uint64_t r = ((uint64_t)rd() << 32) ^ rd() ^ (t * 0x9E3779B97F4A7C15ull);
+    return (r >> 2) | (1ull << 63);  // room for 2^62 launches before the top bit clears
+  }()};
   DecodeArgs a = args;
-  a.epoch = epochs.fetch_add(1, std::memory_order_relaxed) + 1;
+  a.epoch = epochs.fetch_add(1, std::memory_order_relaxed);
   a.merge_wgs = std::max(1, std::min(batch * g.nkv, a.waves / 2));
   a.merge_timeout = kMergeTimeoutTicks;
   a.merge_skew = 0;
-  if (const uint64_t t = test_merge_timeout_ticks()) {
+  if (const uint64_t t = g_test_merge_timeout_ticks.load(std::memory_order_relaxed)) {
     a.merge_timeout = t;
     a.merge_skew = 1;
   }

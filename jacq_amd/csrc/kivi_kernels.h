@@ -54,6 +54,7 @@ struct DecodeArgs {
   uint64_t merge_timeout = 0;  // matrix-core kernel: s_memrealtime ticks a merge waits at most
   uint64_t merge_skew = 0;     // matrix-core kernel: 0; 1 only in the forced-timeout test
   int retained_pages = -1;  // >= 0: sparse-retained window (compact block table)
+  uint32_t* status = nullptr;  // matrix-core kernel: set to 1 when a merge wait runs out
 };
 
 // Decode window of one sequence.  Dense: the split rule (decode_window).
@@ -87,6 +88,10 @@ struct LaunchEvents {
 };
 hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
                               hipStream_t stream, const LaunchEvents& ev = LaunchEvents());
+// Test-only: with us > 0 every later matrix-core decode's merge waits for an
+// epoch no wavefront stores and gives up after `us` microseconds; 0 restores
+// normal operation.
+void set_test_merge_timeout_us(uint32_t us);
 // wavefronts the matrix-core decode launches on a device with `cus` CUs:
 // as many as are resident at once
 int decode_stream_waves(const KiviGeo& g, int cus);

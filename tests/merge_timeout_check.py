@@ -1,11 +1,12 @@
-"""Child process of test_gpu_parity.test_merge_timeout_drains: with
-JACQ_KIVI_TEST_MERGE_TIMEOUT_US set (read once, when the library loads) every
-merge wait of the decode runs out.  Prints, as JSON, how many (sequence, kv
-head) segments came out NaN (merged ones), how many match the oracle (written
-whole by one wavefront) and how many are neither."""
+"""Child process of test_gpu_parity.test_merge_timeout_exits_v1_symbols.
+
+With the library's test hook every merge wait of a decode runs out.  The
+first jac_launch (v1 geometry, one 4096-token sequence, whose split-K pieces
+need merging) returns and drains; the second sees the device's time-out
+status and must print the error and exit(1), as the v1 symbols do for launch
+errors.  Prints FIRST_DECODE_RETURNED between the two calls."""
 from __future__ import annotations
 
-import json
 import os
 import sys
 
@@ -17,34 +18,27 @@ import torch  # noqa: E402
 
 from jacq_amd import kivi  # noqa: E402
 from jacq_amd import workloads as wl  # noqa: E402
-from tests.kivi_testlib import ATOL, RTOL, State, to_torch  # noqa: E402
+from tests.kivi_testlib import State, to_torch  # noqa: E402
 
 
 def main() -> int:
-    assert os.environ.get("JACQ_KIVI_TEST_MERGE_TIMEOUT_US")
-    w = wl.WORKLOADS["qwen14b"]
-    st = State(w, lens=[3000, 129, 20, 700, 1], seed=13)
+    w = wl.Workload("v1", 40, 8, 128, 1, 4096, 4096, page=32, residual=128, seed=11)
+    st = State(w, lens=[4096], seed=4)
     st.build_oracle()
-    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, st.max_pages,
-                            st.num_pages)
-    cache = kivi.PagedKiviCache.from_tensors(geo, to_torch(st))
-    q = torch.from_numpy(st.q).view(torch.float16).cuda()
-    out = cache.decode(q, torch.from_numpy(st.lens.astype(np.int32)).cuda(),
-                       torch.from_numpy(st.tables).cuda())
+    g = to_torch(st)
+    bt = torch.from_numpy(st.tables[0]).cuda()
+    q = torch.from_numpy(st.q[0].copy()).view(torch.float16).cuda()
+    out = torch.empty((40, 128), dtype=torch.float32, device="cuda")
+    pool = [g[n] for n in ("k_code", "k_scale", "k_zero", "v_code", "v_scale", "v_zero")]
+    kivi.lib().jacq_kivi_test_force_merge_timeout(20)
+    kivi.kivi_decode_dsl(q, bt, *pool, g["k_scr"][0], g["v_scr"][0], 4096, out)
     torch.cuda.synchronize()
-    got, ref = out.cpu().numpy().astype(np.float64), st.decode_ref()
-    G = w.nh // w.nkv
-    counts = {"nan": 0, "match": 0, "other": 0}
-    for b in range(st.batch):
-        for h in range(w.nkv):
-            g_, r_ = got[b, h * G:(h + 1) * G], ref[b, h * G:(h + 1) * G]
-            if np.isnan(g_).all():
-                counts["nan"] += 1
-            elif (np.abs(g_ - r_) <= ATOL + RTOL * np.abs(r_)).all():
-                counts["match"] += 1
-            else:
-                counts["other"] += 1
-    print(json.dumps(counts), flush=True)
+    assert np.isnan(out.cpu().numpy()).any(), "the forced time-out merged nothing"
+    print("FIRST_DECODE_RETURNED", flush=True)
+    kivi.lib().jacq_kivi_test_force_merge_timeout(0)
+    kivi.kivi_decode_dsl(q, bt, *pool, g["k_scr"][0], g["v_scr"][0], 4096, out)
+    torch.cuda.synchronize()
+    print("SECOND_DECODE_RETURNED", flush=True)
     return 0
 
 
