@@ -276,6 +276,27 @@ int jacq_kivi_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q,
                      const jacq_half_t* V_RESIDUAL_SCRATCH, int32_t batch, float* O,
                      void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* jacq_kivi_decode with no allocation at all.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as jacq_kivi_decode without the
+ * workspace: the split-K partials go to a static 32 MiB device array of the
+ * library (one copy per GPU, held until the process ends), enough for 256
+ * sequences at the long-context geometry (64/8 heads, HD 128).  A batch that
+ * needs more is refused with JACQ_KIVI_ENOMEM and nothing launched.
+ * jacq_kivi_init() must have run on the device first (its set-up is the only
+ * allocation; otherwise JACQ_KIVI_EINVAL).  Every call on a GPU shares that
+ * GPU's array: calls that can overlap on one GPU (other streams, other
+ * threads) race and must be serialised by the caller. */
+int jacq_kivi_decode_noalloc(const jacq_kivi_geometry* geo, const jacq_half_t* Q,
+                             const int32_t* SEQ_LENS, const int32_t* BLOCK_TABLES,
+                             const uint8_t* K_CODE_PAGES, const jacq_half_t* K_SCALE_PAGES,
+                             const jacq_half_t* K_ZERO_PAGES, const uint8_t* V_CODE_PAGES,
+                             const jacq_half_t* V_SCALE_PAGES, const jacq_half_t* V_ZERO_PAGES,
+                             const jacq_half_t* K_RESIDUAL_SCRATCH,
+                             const jacq_half_t* V_RESIDUAL_SCRATCH, int32_t batch, float* O,
+                             hipStream_t stream);
+
 /* Sparse-retained decode of one sequence at a runtime geometry (the
  * jac_launch_sparse_retained window, variants.rs:2667-2680).
  *   Q                     [NH, HD] fp16

@@ -92,8 +92,16 @@ struct StreamWorkspace {
   void* ptr;
   size_t bytes;
 };
+// Split-K workspace of jacq_kivi_decode_noalloc: a static device array, so
+// that entry point allocates nothing.  Each device holds its own copy (at its
+// own address, from hipGetSymbolAddress at set-up) until the process ends.
+// Zero-initialised; like any workspace it needs no particular contents.
+constexpr size_t kNoAllocScratchBytes = 32u << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 struct DeviceState {
   int cus = 0;
+  void* scratch_ptr = nullptr;  // this device's copy of `scratch`
   // Pinned, host-coherent word the decode kernels set (system-scope vector
   // store) when a split-K merge wait runs out; read by the host without a
   // synchronisation, cleared by jacq_kivi_decode_status.
@@ -128,6 +136,12 @@ int init_device_locked(int dev) {
     s.status = (volatile uint32_t*)p;
     s.status_dev = (uint32_t*)d;
   }
+  if (!s.scratch_ptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr)
+      return fail(JACQ_KIVI_EHIP, "hipGetSymbolAddress(scratch) failed");
+    s.scratch_ptr = ptr;
+  }
   return JACQ_KIVI_OK;
 }
 
@@ -143,11 +157,25 @@ struct DeviceInfo {
   int cus;
   volatile uint32_t* status;
   uint32_t* status_dev;
+  void* scratch_ptr;
 };
 DeviceInfo device_state(int dev) {
   std::lock_guard<std::mutex> lk(g_mu);
   const DeviceState& s = g_dev[dev];
-  return {s.cus, s.status, s.status_dev};
+  return {s.cus, s.status, s.status_dev, s.scratch_ptr};
+}
+
+// Set-up state of the current device without setting it up (nothing is
+// allocated): false when jacq_kivi_init (or any other entry point) has not
+// run on it yet.
+bool device_ready(int* dev, DeviceInfo* info) {
+  if (hipGetDevice(dev) != hipSuccess) return false;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if ((int)g_dev.size() <= *dev) return false;
+  const DeviceState& s = g_dev[*dev];
+  if (!s.status || !s.scratch_ptr) return false;
+  *info = {s.cus, s.status, s.status_dev, s.scratch_ptr};
+  return true;
 }
 
 constexpr const char* kTimeoutMsg =
@@ -446,6 +474,7 @@ int jacq_kivi_decode_status(void* workspace, size_t workspace_bytes_, hipStream_
     std::lock_guard<std::mutex> lk(g_mu);
     all = g_dev[dev].ws;
     all.insert(all.end(), g_dev[dev].retired.begin(), g_dev[dev].retired.end());
+    all.push_back({stream, g_dev[dev].scratch_ptr, kNoAllocScratchBytes});
   }
   if (workspace && workspace_bytes_) all.push_back({stream, workspace, workspace_bytes_});
   for (const auto& w : all)
@@ -509,6 +538,43 @@ int jacq_kivi_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q, const 
                     K_SCALE_PAGES, K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES,
                     K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, scr, batch, O, workspace,
                     workspace_bytes_, stream);
+}
+
+int jacq_kivi_decode_noalloc(const jacq_kivi_geometry* geo, const jacq_half_t* Q,
+                             const int32_t* SEQ_LENS, const int32_t* BLOCK_TABLES,
+                             const uint8_t* K_CODE_PAGES, const jacq_half_t* K_SCALE_PAGES,
+                             const jacq_half_t* K_ZERO_PAGES, const uint8_t* V_CODE_PAGES,
+                             const jacq_half_t* V_SCALE_PAGES, const jacq_half_t* V_ZERO_PAGES,
+                             const jacq_half_t* K_RESIDUAL_SCRATCH,
+                             const jacq_half_t* V_RESIDUAL_SCRATCH, int32_t batch, float* O,
+                             hipStream_t stream) {
+  if (int e = check_geometry(geo)) return e;
+  if (batch < 1) return fail(JACQ_KIVI_EINVAL, "batch must be >= 1");
+  int dev = 0;
+  DeviceInfo ds{};
+  if (!device_ready(&dev, &ds))
+    return fail(JACQ_KIVI_EINVAL,
+                "jacq_kivi_decode_noalloc: call jacq_kivi_init() on this device first "
+                "(its one-time set-up is the only allocation)");
+  const KiviGeo g = make_geo(*geo);
+  const size_t need = workspace_bytes(g, batch, plan_splits(max_seq_len(*geo)),
+                                      jacq::decode_stream_waves(g, ds.cus));
+  if (need > kNoAllocScratchBytes)
+    return fail(JACQ_KIVI_ENOMEM,
+                "jacq_kivi_decode_noalloc: " + std::to_string(batch) +
+                    " sequences at this geometry need " + std::to_string(need) +
+                    " bytes of split-K workspace, above the static " +
+                    std::to_string(kNoAllocScratchBytes) +
+                    "-byte maximum; use jacq_kivi_decode with a workspace");
+  if (!Q || !SEQ_LENS || !K_CODE_PAGES || !K_SCALE_PAGES || !K_ZERO_PAGES || !V_CODE_PAGES ||
+      !V_SCALE_PAGES || !V_ZERO_PAGES || !K_RESIDUAL_SCRATCH || !V_RESIDUAL_SCRATCH || !O ||
+      (!BLOCK_TABLES && geo->max_pages_per_seq > 0))
+    return fail(JACQ_KIVI_EINVAL, "null tensor pointer");
+  const int64_t scr = (int64_t)geo->num_kv_heads * (geo->residual + geo->group_size) * geo->head_dim;
+  return run_decode(*geo, Q, SEQ_LENS, -1, BLOCK_TABLES, geo->max_pages_per_seq, K_CODE_PAGES,
+                    K_SCALE_PAGES, K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES,
+                    K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, scr, batch, O, ds.scratch_ptr,
+                    kNoAllocScratchBytes, stream);
 }
 
 int jacq_kivi_decode_sparse_retained(

@@ -132,6 +132,9 @@ def lib() -> ctypes.CDLL:
     L.jacq_kivi_decode.argtypes = [ctypes.POINTER(Geometry)] + [_vp] * 11 + [
         _i32, _vp, _vp, ctypes.c_size_t, _vp]
     L.jacq_kivi_decode.restype = ctypes.c_int
+    L.jacq_kivi_decode_noalloc.argtypes = [ctypes.POINTER(Geometry)] + [_vp] * 11 + [
+        _i32, _vp, _vp]
+    L.jacq_kivi_decode_noalloc.restype = ctypes.c_int
     L.jacq_kivi_decode_sparse_retained.argtypes = [ctypes.POINTER(Geometry), _vp, _i32, _vp,
                                                    _i32] + [_vp] * 9 + [_vp, ctypes.c_size_t,
                                                                         _vp]
