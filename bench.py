@@ -74,7 +74,7 @@ def main() -> int:
 
     import torch
 
-    from jacq_amd import kivi, layout, workloads as wl
+    from jacq_amd import geometry, kivi, workloads as wl
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
@@ -183,7 +183,7 @@ def main() -> int:
     kern, _, _, _, _ = timed_pass(total_steps, split=True)
 
     def bytes_of(step0):
-        return [layout.decode_step_bytes(lens0 + step0 + i + 1, w.nh, w.nkv, w.hd, w.page,
+        return [geometry.decode_step_bytes(lens0 + step0 + i + 1, w.nh, w.nkv, w.hd, w.page,
                                          w.residual, w.group)
                 for i in range(args.warmup, total_steps)]
     step_bytes = bytes_of(0)
@@ -202,7 +202,7 @@ def main() -> int:
         last = 2 * total_steps  # the state after the last decode of pass 2
         cpu = cpu_baseline(args, w, cache, qs[last - 1], lens0 + last, tables_np,
                            out, max_pages,
-                           bytes_per_step_last=layout.decode_step_bytes(
+                           bytes_per_step_last=geometry.decode_step_bytes(
                                lens0 + last, w.nh, w.nkv, w.hd, w.page, w.residual, w.group))
 
     traffic = load_traffic(args.workload)

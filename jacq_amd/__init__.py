@@ -5,6 +5,6 @@ reference's callable C launch contract (include/jacq_kivi.h).
 The native library is ``jacq_amd/libjacq_kivi.so`` (``python -m jacq_amd.build``).
 ``jacq_amd.kivi`` binds it; there is no CPU fallback.
 """
-from jacq_amd import abi, bindings, layout  # noqa: F401
+from jacq_amd import abi, geometry  # noqa: F401
 
-__all__ = ["abi", "bindings", "layout", "kivi", "cache_io", "workloads"]
+__all__ = ["abi", "geometry", "kivi", "cache_io", "workloads"]

@@ -9,12 +9,12 @@ is the reference's, unchanged; the runtime-geometry surface
 """
 from __future__ import annotations
 
-from jacq_amd.bindings import KiviDecodeBindingAbi, default_qwen32b_binding_abi
-from jacq_amd.layout import KiviModelGeometry
+from jacq_amd import geometry as geo
 
 
 class UnsupportedAbiError(Exception):
-    """Raised when a request or environment violates a hard ABI boundary."""
+    """A GPU, geometry or length outside what this build's v1 surface serves;
+    the message names the limit that was crossed."""
 
 
 JACQ_KIVI_ABI_VERSION = 1   # abi.py:36 -- the reference launch contract
@@ -23,10 +23,10 @@ JACQ_KIVI_EXT_VERSION = 1   # additive jacq_kivi_* runtime-geometry surface
 # The one validated architecture: MI355X (CDNA4).  abi.py:45 lists sm_80/sm_89.
 SUPPORTED_GPU_ARCHES = ("gfx950",)
 
-OLD_BLOCKS_CAP = 124
-BLOCK_SIZE = 32
-RESIDUAL_TOKENS = 128
-MAX_SEQ_LEN = OLD_BLOCKS_CAP * BLOCK_SIZE + RESIDUAL_TOKENS  # 4096
+OLD_BLOCKS_CAP = geo.V1.max_pages_per_seq
+BLOCK_SIZE = geo.V1.page_size
+RESIDUAL_TOKENS = geo.V1.residual
+MAX_SEQ_LEN = geo.V1_MAX_SEQ_LEN  # 4096
 
 # C symbols a caller binds (include/jacq_kivi.h); abi.py:58-62 lists the
 # torch ops that wrap them.
@@ -45,8 +45,8 @@ REQUIRED_OPS = ("kivi_cache_write_dsl", "kivi_cache_write_jac_dsl", "kivi_decode
 CACHE_WRITE_KERNELS = ("hand_cuda", "jac_dsl")  # selector values kept for drop-in callers
 
 
-def supported_geometry() -> KiviModelGeometry:
-    return KiviModelGeometry.qwen25_coder_32b()
+def supported_geometry() -> geo.LaneGeometry:
+    return geo.V1
 
 
 def check_gpu_arch(arch: str) -> None:
@@ -60,48 +60,46 @@ def check_gpu_arch(arch: str) -> None:
             "Refusing to run.")
 
 
-def check_geometry(geometry: KiviModelGeometry) -> None:
-    """v1 lane: only the 40/8/128 geometry (abi.py:186-197)."""
-    expected = supported_geometry()
-    for attr in ("num_attention_heads", "num_kv_heads", "head_dim"):
-        got, want = getattr(geometry, attr), getattr(expected, attr)
+def check_geometry(g: geo.LaneGeometry) -> None:
+    """v1 lane: only the 40/8/128 head geometry (abi.py:186-197)."""
+    for attr in ("num_heads", "num_kv_heads", "head_dim"):
+        got, want = getattr(g, attr), getattr(geo.V1, attr)
         if got != want:
             raise UnsupportedAbiError(
-                f"model geometry {attr}={got} does not match the supported lane "
-                f"({expected.name}: {attr}={want}); fail closed.")
+                f"{attr}={got}: the v1 symbols are built for {want} (40 query / 8 kv heads, "
+                "head_dim 128); use the jacq_kivi_* runtime-geometry entry points")
 
 
-def _checked_binding(seq_len: int) -> KiviDecodeBindingAbi:
+def _check_seq_len(seq_len: int) -> None:
     if seq_len > MAX_SEQ_LEN:
         raise UnsupportedAbiError(
-            f"seq_len {seq_len} exceeds the KIVI ABI v1 cap of {MAX_SEQ_LEN} "
-            f"({OLD_BLOCKS_CAP} old pages x {BLOCK_SIZE} tokens + {RESIDUAL_TOKENS}-token "
-            "residual). Use the runtime-geometry jacq_kivi_* surface for longer contexts.")
-    return default_qwen32b_binding_abi(seq_len=seq_len)
+            f"seq_len {seq_len} is beyond the v1 limit of {MAX_SEQ_LEN} tokens "
+            f"({OLD_BLOCKS_CAP} table entries x {BLOCK_SIZE} + {RESIDUAL_TOKENS} fp16 tokens); "
+            "the jacq_kivi_* entry points take wider block tables")
+
+
+WRITE_ORDER = ("K_CODE_PAGES", "K_SCALE_PAGES", "K_ZERO_PAGES", "V_CODE_PAGES", "V_SCALE_PAGES",
+               "V_ZERO_PAGES", "K_RESIDUAL_SCRATCH", "V_RESIDUAL_SCRATCH", "NEW_K", "NEW_V",
+               "BLOCK_TABLE", "SEQ_LEN", "hipStream_t stream")
 
 
 def kernel_interface(seq_len: int = MAX_SEQ_LEN) -> dict:
     """The versioned callable surface for one decode step (abi.py:74-112)."""
-    abi = _checked_binding(seq_len)
+    _check_seq_len(seq_len)
     return {
         "abi_version": JACQ_KIVI_ABI_VERSION,
         "ext_version": JACQ_KIVI_EXT_VERSION,
         "supported_gpu_arches": list(SUPPORTED_GPU_ARCHES),
         "required_ops": list(REQUIRED_OPS),
         "cache_write_kernels": list(CACHE_WRITE_KERNELS),
-        "seq_len": abi.seq_len,
-        "old_pages": abi.old_pages,
+        "seq_len": seq_len,
+        "old_pages": geo.V1.old_tokens(seq_len) // geo.V1.page_size,
         "symbols": {"v1": list(V1_SYMBOLS), "ext": list(EXT_SYMBOLS)},
         "kernels": [
             {"op": "kivi_decode_dsl", "symbol": "jac_launch",
-             "launch_order": abi.jac_launch_order()},
+             "launch_order": list(geo.JAC_LAUNCH_ORDER)},
             {"op": "kivi_cache_write_jac_dsl", "symbol": "jac_launch_cache_write",
-             "launch_order": ["K_CODE_PAGES", "K_SCALE_PAGES", "K_ZERO_PAGES", "V_CODE_PAGES",
-                              "V_SCALE_PAGES", "V_ZERO_PAGES", "K_RESIDUAL_SCRATCH",
-                              "V_RESIDUAL_SCRATCH", "NEW_K", "NEW_V", "BLOCK_TABLE", "SEQ_LEN",
-                              "hipStream_t stream"]},
+             "launch_order": list(WRITE_ORDER)},
         ],
-        "integrity_boundary": (
-            "This describes the callable surface only; it allocates nothing and launches "
-            "nothing. Numerical parity is established by the GPU tests against the CPU oracle."),
+        "note": "describes the callable surface only; nothing is allocated or launched",
     }

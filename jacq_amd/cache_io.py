@@ -1,7 +1,8 @@
 """Cache dump / load: one self-describing file per paged KIVI cache state.
 
 The byte layouts are the v1 ones the kernels read (layout.py:42-154 of the
-reference gives the per-page byte math; ``jacq_amd.layout`` restates it):
+reference gives the per-page byte math; ``jacq_amd.geometry.page_bytes``
+computes it):
 
 * ``k_code`` / ``v_code``   uint8   [pages, NKV, page, HD/2]   (two int4 codes a byte,
   even channel in the low nibble)

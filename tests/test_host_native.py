@@ -24,7 +24,7 @@ import numpy as np
 import pytest
 import torch
 
-from jacq_amd import abi, bindings, kivi, layout
+from jacq_amd import abi, geometry, kivi
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "jacq_kivi.h")
@@ -90,7 +90,7 @@ def test_jac_launch_argument_order_matches_reference():
     assert params == ["Q", "BLOCK_TABLE", "K_CODE_PAGES", "K_SCALE_PAGES", "K_ZERO_PAGES",
                       "V_CODE_PAGES", "V_SCALE_PAGES", "V_ZERO_PAGES", "K_RESIDUAL_SCRATCH",
                       "V_RESIDUAL_SCRATCH", "SEQ_LEN", "O", "stream"]
-    order = list(bindings.JAC_LAUNCH_ORDER)
+    order = list(geometry.JAC_LAUNCH_ORDER)
     assert order[:-1] == params[:-1] and order[-1].endswith("stream")
     assert "K_RESIDUAL" not in order and "V_RESIDUAL" not in order
     # source_patch.py:589-595: the dense order with RETAINED_BLOCK_TABLE and
@@ -173,24 +173,40 @@ def test_geometry_accept_reject(native, kw, ok):
 
 
 def test_layout_byte_math_matches_reference_fixture():
-    lay = layout.KiviPageLayout(layout.KiviModelGeometry.qwen25_coder_32b())
-    d = lay.to_abi_dict(seq_len=4096)
-    assert d["fp16_page_bytes_per_layer"] == 131_072
-    assert d["key_code_bytes"] == 16_384 and d["value_code_bytes"] == 16_384
-    assert d["key_scale_zero_bytes"] == 4_096 and d["value_scale_zero_bytes"] == 4_096
-    assert d["quantized_page_bytes_per_layer"] == 40_960
-    assert d["residual_pages"] == 4
-    assert d["effective_bytes_per_token_all_layers_at_seq_len"] == 87_552.0
-    assert 2.99 < d["capacity_ratio_vs_fp16_at_seq_len"] < 3.0
-    with pytest.raises(ValueError, match="block_size==group_size"):
-        layout.KiviPageLayout(layout.KiviModelGeometry.qwen25_coder_32b(),
-                              block_size=16).validate_for_vllm_lane()
+    """tests/test_layout_and_scaffold.py:162-179 of the reference, at its lane
+    geometry (Qwen2.5-Coder-32B: 64 layers, 40/8 heads, HD 128, page 32)."""
+    pb = geometry.page_bytes(geometry.V1)
+    assert pb["fp16_equivalent"] == 131_072
+    assert pb["k_codes"] == 16_384 and pb["v_codes"] == 16_384
+    assert pb["k_params"] == 4_096 and pb["v_params"] == 4_096
+    assert pb["total"] == 40_960
+    assert geometry.V1.residual // geometry.V1.page_size == 4
+    assert geometry.stored_bytes_per_token(geometry.V1, 4096, 64) == 87_552.0
+    assert 2.99 < geometry.capacity_vs_fp16(geometry.V1, 4096, 64) < 3.0
+    with pytest.raises(ValueError, match="straddle"):
+        geometry.LaneGeometry(40, 8, 128, page_size=16).require("v1")
+    geometry.LaneGeometry(40, 8, 128, page_size=16).require("runtime")
+    # page 16: a key group's pairs are stored on both of its pages
+    p16 = geometry.page_bytes(geometry.LaneGeometry(40, 8, 128, page_size=16))
+    assert p16["k_params"] == 4_096 and p16["k_codes"] == 8_192
+
+
+def test_launch_argument_table_matches_the_header(native):
+    """The Python argument table and include/jacq_kivi.h name the same
+    arguments in the same order, and their byte sizes follow the layout."""
+    assert list(geometry.JAC_LAUNCH_ORDER[:-1]) == header_functions()["jac_launch"][:-1]
+    b = geometry.argument_bytes(geometry.V1, pool_pages=124)
+    assert b["K_CODE_PAGES"] == 124 * 16_384 and b["V_SCALE_PAGES"] == 124 * 2_048
+    assert b["K_RESIDUAL_SCRATCH"] == 8 * 160 * 128 * 2 and b["O"] == 40 * 128 * 4
 
 
 def test_decode_bytes_formula():
     """160 bytes per token per kv head at HD=128, 80 at HD=64 (quantised part)."""
-    assert layout.decode_kv_bytes_per_token(128) == 160
-    assert layout.decode_kv_bytes_per_token(64) == 80
+    assert geometry.decode_kv_bytes_per_token(128) == 160
+    assert geometry.decode_kv_bytes_per_token(64) == 80
+    # one sequence of 4096 at the v1 shape: 3968 quantised, 128 fp16 tokens
+    n = geometry.decode_step_bytes([4096], 40, 8, 128, 32, 128)
+    assert n == 8 * (3968 * 160 + 128 * 512) + 4 * 124 + 40 * 128 * 6
 
 
 def check_plan(plan, start, num, residual, group):
