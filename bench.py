@@ -311,14 +311,19 @@ def cpu_baseline(args, w, cache, q_last, lens_last, tables_np, gpu_out, max_page
                 host(cache.k_scr), host(cache.v_scr))
     q = host(q_last)
     lens = lens_last.astype(np.int32)
-    threads = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
+    affinity = len(os.sched_getaffinity(0))
+    threads = args.cpu_threads or min(16, affinity)
     t0 = time.perf_counter()
     ref = o.decode_batch(c, q, lens, tables_np, nthreads=threads)
     dt = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    ref1 = o.decode_batch(c, q, lens, tables_np, nthreads=1)
+    dt1 = time.perf_counter() - t0
     # sanity: the GPU's last step saw the same state and query
     gpu = gpu_out.cpu().numpy()
     err = np.abs(gpu - ref)
-    ok = bool(np.all(err <= ATOL + RTOL * np.abs(ref)))
+    bound = ATOL + RTOL * np.abs(ref)
+    ok = bool(np.all(err <= bound))
     return {
         "value": round(bytes_per_step_last / dt / 1e9, 3),
         "unit": "GB/s",
@@ -326,11 +331,29 @@ def cpu_baseline(args, w, cache, q_last, lens_last, tables_np, gpu_out, max_page
         "kind": "port",
         "sample": f"full last step: {w.batch} sequences, one decode query each, "
                   f"{int(lens.sum())} tokens; {dt * 1e3:.1f} ms on {threads} threads "
-                  f"(OpenMP over sequence x kv head)",
+                  f"(OpenMP over sequence x kv head), {dt1 * 1e3:.1f} ms on 1 thread",
         "us_per_step": round(dt * 1e6, 1),
+        "single_thread": {"value": round(bytes_per_step_last / dt1 / 1e9, 3), "unit": "GB/s",
+                          "us_per_step": round(dt1 * 1e6, 1),
+                          "same_result": bool(np.array_equal(ref, ref1))},
+        "host": {"nproc": os.cpu_count(), "affinity_cpus": affinity,
+                 "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS"),
+                 "cpu_model": cpu_model()},
         "matches_gpu_within_tolerance": ok,
         "max_abs_diff_vs_gpu": float(err.max()),
+        "max_err_over_bound": round(float((err / bound).max()), 4),
     }
+
+
+def cpu_model() -> str | None:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 if __name__ == "__main__":

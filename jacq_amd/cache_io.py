@@ -92,6 +92,12 @@ def live_pages(geo: KiviGeometry, block_tables: np.ndarray, seq_lens: np.ndarray
     return np.fromiter(seen.keys(), dtype=np.int64, count=len(seen))
 
 
+def _check_lens(geo: KiviGeometry, sl: torch.Tensor, what: str) -> None:
+    if (sl < 0).any() or (sl > geo.max_seq_len()).any():
+        raise ValueError(f"{what} outside [0, {geo.max_seq_len()}]: the decode would clamp "
+                         "them, the file format stores only lengths in range")
+
+
 def _digest(t: torch.Tensor) -> str:
     return hashlib.sha256(t.contiguous().view(torch.uint8).numpy().tobytes()).hexdigest()
 
@@ -110,6 +116,7 @@ def dump_cache(path: str, cache: PagedKiviCache, block_tables: torch.Tensor,
                          f"got {list(bt.shape)}")
     if tuple(sl.shape) != (batch,):
         raise ValueError(f"seq_lens must be [{batch}], got {list(sl.shape)}")
+    _check_lens(geo, sl, "seq_lens")  # the rule load_cache applies, so every dump loads
     tensors = {k: getattr(cache, k).detach().to("cpu").contiguous() for k in POOL + SCRATCH}
     pages = live_pages(geo, bt.numpy(), sl.numpy())  # raises on an entry outside the pool
     if compact:
@@ -180,8 +187,7 @@ def load_cache(path: str, device="cpu"):
         if _digest(t) != digests.get(k):
             raise ValueError(f"{path}: {k} does not match its SHA-256")
     sl = tensors["seq_lens"]
-    if (sl < 0).any() or (sl > geo.max_seq_len()).any():
-        raise ValueError(f"{path}: seq_lens outside [0, {geo.max_seq_len()}]")
+    _check_lens(geo, sl, f"{path}: seq_lens")
     live_pages(geo, tensors["block_tables"].numpy(), sl.numpy())  # raises on a bad entry
     dev = torch.device(device)
     cache = PagedKiviCache.from_tensors(geo, {k: tensors[k].to(dev) for k in POOL + SCRATCH})

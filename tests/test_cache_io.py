@@ -155,6 +155,23 @@ def test_dump_rejects_out_of_pool_tables(tmp_path):
         cache_io.dump_cache(str(tmp_path / "x.safetensors"), _cache(st), bt, _lens(st))
 
 
+def test_dump_rejects_lengths_load_would_reject(tmp_path):
+    """dump_cache and load_cache apply one length rule, so every file dump
+    writes loads back: a negative length or one past max_seq_len is refused
+    at dump time (the decode would clamp it; the format does not store it)."""
+    st = _state("qwen05b", (300,))
+    geo = _kgeo(st)
+    for bad in (-1, geo.max_seq_len() + 1):
+        with pytest.raises(ValueError, match="outside"):
+            cache_io.dump_cache(str(tmp_path / "x.safetensors"), _cache(st),
+                                torch.from_numpy(st.tables), torch.tensor([bad], dtype=torch.int32))
+    p = str(tmp_path / "edge.safetensors")
+    cache_io.dump_cache(p, _cache(st), torch.from_numpy(st.tables),
+                        torch.tensor([geo.max_seq_len()], dtype=torch.int32))
+    _, _, sl = cache_io.load_cache(p)
+    assert int(sl[0]) == geo.max_seq_len()
+
+
 @pytest.mark.gpu
 def test_gpu_written_cache_round_trips_and_decodes_identically(tmp_path):
     """HIP writer builds the state; after a compact dump and a reload on the
