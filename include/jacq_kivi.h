@@ -19,7 +19,8 @@
  *
  * Conventions (both groups):
  *  - every pointer is caller-owned device memory.  The library allocates
- *    only split-K workspaces for the decodes, one per (device, stream): the v1 decode
+ *    twice: a pinned status word per device (jacq_kivi_init), and split-K
+ *    workspaces for the decodes, one per (device, stream): the v1 decode
  *    symbols always use them, the jacq_kivi_* decodes when the caller passes
  *    none.  A stream's workspace is allocated on its first decode for at
  *    least 256 sequences and replaced by a larger one when a larger batch
@@ -187,6 +188,7 @@ void kivi_cache_write_batched_launch(uint8_t* K_CODE_PAGES, jacq_half_t* K_SCALE
 #define JACQ_KIVI_EINVAL 1   /* argument outside the supported contract */
 #define JACQ_KIVI_EHIP 2     /* a HIP runtime call failed */
 #define JACQ_KIVI_ENOMEM 3   /* workspace allocation failed / too small */
+#define JACQ_KIVI_ETIMEOUT 4 /* a split-K merge wait of an earlier decode ran out */
 
 typedef struct jacq_kivi_geometry {
   int32_t num_heads;         /* NH */
@@ -207,11 +209,32 @@ int jacq_kivi_ext_version(void);
 const char* jacq_kivi_last_error(void);
 
 /* Per-device set-up of the current device (no counterpart in the reference,
- * whose symbols keep no state): device properties and the address of the
- * library's static decode scratch.  Allocates nothing.  Every entry point
- * does it on its first call on a device; jacq_kivi_decode_noalloc requires
- * that it has run. */
+ * whose symbols keep no state): device properties and a pinned status word
+ * the decode kernels set when a split-K merge times out.  Every entry point
+ * does it on its first call on a device; calling it first keeps that
+ * one-time host allocation out of later calls (and out of graph captures). */
 int jacq_kivi_init(void);
+
+/* Merge time-out status of the current device (no counterpart in the
+ * reference).  A decode's split-K merge waits at most 1 s for the partials of
+ * its own launch; if that runs out (its stream wavefronts never ran, e.g.
+ * starved on a shared device) it writes NaN for the merged outputs and sets
+ * the device's status word.  While the word is set, every jacq_kivi_* decode
+ * returns JACQ_KIVI_ETIMEOUT without launching and every v1 decode symbol
+ * prints the error and exits(1), as its other launch errors do.  This call
+ * synchronises `stream`, and when the word is set it waits for the device,
+ * zeroes every workspace the library owns on the device and `workspace`
+ * (when not NULL; flags a timed-out merge left behind would otherwise be read
+ * by a graph replay carrying the same epoch), clears the word and returns
+ * JACQ_KIVI_ETIMEOUT; otherwise JACQ_KIVI_OK.  Call it with no decode running
+ * on the device. */
+int jacq_kivi_decode_status(void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Test hook (no counterpart in the reference): with microseconds > 0 every
+ * later matrix-core decode's merge waits for a tag that no wavefront stores
+ * and gives up after that long, so tests can force the time-out path from the
+ * host (every kernel still exits normally).  0 restores normal operation. */
+void jacq_kivi_test_force_merge_timeout(uint32_t microseconds);
 
 /* Geometry check (integrations/vllm_kivi/layout.py:51-74 and the supported
  * geometry checks of source_patch.py:744-756, generalised). */
@@ -237,13 +260,12 @@ size_t jacq_kivi_decode_workspace_size(const jacq_kivi_geometry* geo, int32_t ba
  *   K/V_SCR       [batch, NKV, R+32, HD] fp16
  *   O             [batch, NH, HD] fp32
  * workspace may be NULL (the library then uses its own for `stream`) or at
- * least jacq_kivi_decode_workspace_size bytes.  A caller's workspace must be
- * zero-filled before its first use: its last bytes hold one counter per
- * (sequence, kv head) that the split-K merge uses, and every decode leaves
- * them zero again, so later calls with the same geometry and batch need no
- * clearing (zero it again before using it with another geometry or batch,
- * or after using it for anything else).  Two calls that can run at the same
- * time must not share a workspace.  Sequence lengths are clamped to [0, jacq_kivi_max_seq_len] on the
+ * least jacq_kivi_decode_workspace_size bytes.  Its contents on entry do not
+ * matter: the split-K partials a call stores are tagged with that call's
+ * 64-bit launch epoch (random start, top bit set) and each flag is cleared
+ * when read.  Two calls that can run at the same time must not share a
+ * workspace.  Returns JACQ_KIVI_ETIMEOUT, launching nothing, while the
+ * device's merge status is set (jacq_kivi_decode_status).  Sequence lengths are clamped to [0, jacq_kivi_max_seq_len] on the
  * device, as the reference kernel clamps (snapshot :74-83). */
 int jacq_kivi_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q,
                      const int32_t* SEQ_LENS, const int32_t* BLOCK_TABLES,
@@ -345,16 +367,6 @@ int32_t jacq_kivi_plan_batched_write(int32_t start_seq_len, int32_t num_new, int
  * merge_ms zero.  jacq_kivi_profile_write_ms then writes the per-call
  * milliseconds of the cache-write kernel recorded in the same window. */
 int jacq_kivi_profile_start(int32_t max_calls, int32_t split);
-/* Per-workgroup timing of the matrix-core decode (profiling; no counterpart
- * in the reference).  While `buffer` (device memory, 4 uint64 per workgroup)
- * is not NULL, every later decode launch's workgroup b < capacity writes
- * buffer[4b..4b+3] = {start, end} in s_memrealtime ticks (100 MHz), its
- * HW_ID | XCC_ID << 32, and a packed word: the work units it processed (bits
- * 0-15; 0 for the merge workgroups, which follow the stream wavefronts), the
- * (sequence, kv head) segments it touched (bits 16-23), the fp16 residual
- * tiles it processed (bits 24-31) and the ticks from its start until its
- * first quantised group was in LDS (bits 32-63).  NULL turns it off. */
-int jacq_kivi_profile_wave_stamps(uint64_t* buffer, int32_t capacity);
 int32_t jacq_kivi_profile_stop(float* kernel_ms, float* merge_ms, int32_t cap);
 int32_t jacq_kivi_profile_write_ms(float* ms, int32_t cap);
 

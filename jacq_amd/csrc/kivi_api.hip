@@ -81,32 +81,32 @@ KiviGeo make_geo(const jacq_kivi_geometry& x) {
   return g;
 }
 
-// ---- per-device state: CU count, the static scratch, library workspaces ----
-
-// Split-K workspace of jacq_kivi_decode_noalloc: a static device array, so
-// that entry point allocates nothing.  Each device holds its own copy (at its
-// own address, from hipGetSymbolAddress at set-up) until the process ends.
-// Zero-initialised, which its landed-piece counters require.
-constexpr size_t kNoAllocScratchBytes = 32u << 20;
-static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+// ---- per-device state: CU count, merge status word, library workspaces ----
 
 // A library-owned split-K workspace, one per (device, stream): decodes on
 // different streams may run at the same time and must not share partial
 // slots.  An outgrown buffer is never freed (a captured graph may still hold
 // its address); it moves to `retired` and lives until the process ends.
-// zero_from: the buffer's bytes from there to its end are known to be zero
-// (the landed-piece counters sit at the end of the buffer, and every decode
-// leaves them zero).
 struct StreamWorkspace {
   hipStream_t stream;
   void* ptr;
   size_t bytes;
-  size_t zero_from;
 };
+// Split-K workspace of jacq_kivi_decode_noalloc: a static device array, so
+// that entry point allocates nothing.  Each device holds its own copy (at its
+// own address, from hipGetSymbolAddress at set-up) until the process ends.
+// Zero-initialised; like any workspace it needs no particular contents.
+constexpr size_t kNoAllocScratchBytes = 32u << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 struct DeviceState {
   int cus = 0;
   void* scratch_ptr = nullptr;  // this device's copy of `scratch`
-  size_t scratch_zero_from = 0; // `scratch` starts zeroed
+  // Pinned, host-coherent word the decode kernels set (system-scope vector
+  // store) when a split-K merge wait runs out; read by the host without a
+  // synchronisation, cleared by jacq_kivi_decode_status.
+  volatile uint32_t* status = nullptr;
+  uint32_t* status_dev = nullptr;  // the same word, as the device addresses it
   std::vector<StreamWorkspace> ws;
   std::vector<StreamWorkspace> retired;
 };
@@ -114,7 +114,7 @@ std::mutex g_mu;
 std::vector<DeviceState> g_dev;
 
 // Per-device set-up, once, with the device current.  Called by every entry
-// point (and by jacq_kivi_init); it allocates nothing.
+// point (and by jacq_kivi_init); everything it allocates lives until exit.
 int init_device_locked(int dev) {
   if ((int)g_dev.size() <= dev) g_dev.resize(dev + 1);
   DeviceState& s = g_dev[dev];
@@ -124,6 +124,17 @@ int init_device_locked(int dev) {
         cus <= 0)
       cus = 256;
     s.cus = cus;
+  }
+  if (!s.status) {
+    void* p = nullptr;
+    if (hipHostMalloc(&p, 64, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess || !p)
+      return fail(JACQ_KIVI_ENOMEM, "hipHostMalloc of the decode status word failed");
+    void* d = nullptr;
+    if (hipHostGetDevicePointer(&d, p, 0) != hipSuccess || !d)
+      return fail(JACQ_KIVI_EHIP, "hipHostGetDevicePointer(status word) failed");
+    *(volatile uint32_t*)p = 0;
+    s.status = (volatile uint32_t*)p;
+    s.status_dev = (uint32_t*)d;
   }
   if (!s.scratch_ptr) {
     void* ptr = nullptr;
@@ -144,45 +155,52 @@ int current_device(int* dev) {
 // other threads, so every read takes the lock).
 struct DeviceInfo {
   int cus;
+  volatile uint32_t* status;
+  uint32_t* status_dev;
   void* scratch_ptr;
 };
 DeviceInfo device_state(int dev) {
   std::lock_guard<std::mutex> lk(g_mu);
   const DeviceState& s = g_dev[dev];
-  return {s.cus, s.scratch_ptr};
+  return {s.cus, s.status, s.status_dev, s.scratch_ptr};
 }
 
-// Set-up state of the current device without setting it up: false when
-// jacq_kivi_init (or any other entry point) has not run on it yet.
+// Set-up state of the current device without setting it up (nothing is
+// allocated): false when jacq_kivi_init (or any other entry point) has not
+// run on it yet.
 bool device_ready(int* dev, DeviceInfo* info) {
   if (hipGetDevice(dev) != hipSuccess) return false;
   std::lock_guard<std::mutex> lk(g_mu);
   if ((int)g_dev.size() <= *dev) return false;
   const DeviceState& s = g_dev[*dev];
-  if (!s.scratch_ptr) return false;
-  *info = {s.cus, s.scratch_ptr};
+  if (!s.status || !s.scratch_ptr) return false;
+  *info = {s.cus, s.status, s.status_dev, s.scratch_ptr};
   return true;
 }
+
+constexpr const char* kTimeoutMsg =
+    "a split-K merge of an earlier decode on this device timed out and wrote NaN "
+    "(its stream wavefronts never ran); call jacq_kivi_decode_status() to reset";
 
 // Sequences the library's own split-K workspace covers from its first use
 // (about 13 MB at the v1 geometry).
 constexpr int kLibraryWorkspaceBatch = 256;
 
-int library_workspace(int dev, hipStream_t stream, size_t bytes, void** out, size_t* out_bytes) {
+int library_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
   std::lock_guard<std::mutex> lk(g_mu);
   DeviceState& s = g_dev[dev];
   StreamWorkspace* w = nullptr;
   for (auto& x : s.ws)
     if (x.stream == stream) w = &x;
   if (!w) {
-    s.ws.push_back({stream, nullptr, 0, 0});
+    s.ws.push_back({stream, nullptr, 0});
     w = &s.ws.back();
   }
   if (w->bytes < bytes) {
     if (w->ptr) s.retired.push_back(*w);
     w->ptr = nullptr;
     w->bytes = 0;
-    const size_t want = (bytes + bytes / 4 + 255) & ~(size_t)255;
+    const size_t want = bytes + bytes / 4;
     void* p = nullptr;
     // The first decode on a stream may be inside a stream capture (a graph
     // captured on a fresh stream); an allocation is not a stream operation,
@@ -195,29 +213,13 @@ int library_workspace(int dev, hipStream_t stream, size_t bytes, void** out, siz
     if (me != hipSuccess)
       return fail(JACQ_KIVI_ENOMEM, "hipMalloc of " + std::to_string(want) +
                                          " workspace bytes failed");
+    // Not cleared: a flag counts only when it equals the launch's epoch (a
+    // random 64-bit value with the top bit set), and a synchronous memset
+    // could not run inside a stream capture, where this allocation may happen.
     w->ptr = p;
     w->bytes = want;
-    w->zero_from = want;  // nothing known to be zero yet
   }
   *out = w->ptr;
-  *out_bytes = w->bytes;
-  return JACQ_KIVI_OK;
-}
-
-// Before a decode that uses a library-owned buffer (a stream workspace or the
-// static scratch): its counters, the last `cbytes` bytes (from `cstart`), must
-// be zero.  Bytes from zero_from on are; the rest is cleared with a kernel on
-// the decode's stream (no memset node: the call may be under graph capture).
-// After the decode the counters are zero again, and the partials may have
-// written anything below `data_end`.
-int prepare_counters(void* ptr, size_t* zero_from, size_t cstart, size_t data_end,
-                     hipStream_t stream) {
-  if (cstart < *zero_from) {
-    if (jacq::launch_zero((char*)ptr + cstart, *zero_from - cstart, stream) != hipSuccess)
-      return fail(JACQ_KIVI_EHIP, "workspace clear launch failed");
-    *zero_from = cstart;
-  }
-  if (data_end > *zero_from) *zero_from = data_end;
   return JACQ_KIVI_OK;
 }
 
@@ -249,35 +251,25 @@ size_t partial_slots(const KiviGeo& g, int batch, const SplitPlan& sp, int waves
   return (size_t)batch * g.nkv + (size_t)waves;
 }
 
-// Workspace: from the start, [m,l fp32 per slot and head][acc fp32 per slot,
-// head, channel]; for the matrix-core kernel, at the end of the buffer, one
-// uint32 per (sequence, kv head) counting the landed pieces of a cut segment
-// (8-byte aligned).  The counters must be zero when a decode starts, and every
-// matrix-core decode leaves them zero.
-size_t data_bytes(const KiviGeo& g, int batch, const SplitPlan& sp, int waves) {
-  return partial_slots(g, batch, sp, waves) * g.gqa * (size_t)(g.hd + 2) * sizeof(float);
-}
-size_t counter_bytes(const KiviGeo& g, int batch) {
-  if (use_simple_decode()) return 0;
-  return ((size_t)batch * g.nkv * sizeof(uint32_t) + 7) & ~(size_t)7;
-}
+// Workspace: [m,l fp32 per slot and head][acc fp32 per slot, head, channel]
+// and, for the matrix-core kernel, [epoch uint64 per slot] (8-byte aligned:
+// G * (HD + 2) floats per slot is even).  The flags need no initial contents:
+// a flag counts only when it holds the current launch's 64-bit epoch.
 size_t workspace_bytes(const KiviGeo& g, int batch, const SplitPlan& sp, int waves) {
-  return data_bytes(g, batch, sp, waves) + counter_bytes(g, batch);
-}
-// offset of the counters in a buffer of `total` bytes
-size_t counter_start(const KiviGeo& g, int batch, size_t total) {
-  return (total - counter_bytes(g, batch)) & ~(size_t)7;
+  const size_t slots = partial_slots(g, batch, sp, waves);
+  const size_t flags = use_simple_decode() ? 0 : slots * sizeof(uint64_t);
+  return slots * g.gqa * (size_t)(g.hd + 2) * sizeof(float) + flags;
 }
 
 void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& sp, int waves,
-             void* ws, size_t total) {
+             void* ws) {
   a.max_splits = sp.max_splits;
   a.batch = batch;
   a.waves = waves;
   const size_t slots = partial_slots(g, batch, sp, waves) * g.gqa;
   a.ws_ml = (float*)ws;
   a.ws_acc = ws ? a.ws_ml + slots * 2 : nullptr;
-  a.ws_count = ws ? (uint32_t*)((char*)ws + counter_start(g, batch, total)) : nullptr;
+  a.ws_flag = ws ? (uint64_t*)(a.ws_acc + slots * g.hd) : nullptr;
 }
 
 // ---- measurement hook: HIP events around the decode ----
@@ -330,14 +322,14 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
                const jacq_half_t* ksc, const jacq_half_t* kz, const uint8_t* vc,
                const jacq_half_t* vsc, const jacq_half_t* vz, const jacq_half_t* kscr,
                const jacq_half_t* vscr, int64_t scr_stride, int batch, float* O, void* ws,
-               size_t ws_bytes, hipStream_t stream, int retained_pages = -1,
-               bool is_scratch = false) {
+               size_t ws_bytes, hipStream_t stream, int retained_pages = -1) {
   if (!aligned16({Q, O, kc, ksc, kz, vc, vsc, vz, kscr, vscr, ws}))
     return fail(JACQ_KIVI_EINVAL, "tensor and workspace pointers must be 16-byte aligned");
   const KiviGeo g = make_geo(x);
   int dev = 0;
   if (int e = current_device(&dev)) return e;
   const DeviceInfo ds = device_state(dev);
+  if (*ds.status != 0) return fail(JACQ_KIVI_ETIMEOUT, kTimeoutMsg);
   int64_t max_tokens = max_seq_len(x);
   if (seq_len_host >= 0) {
     int ov, rv;
@@ -354,23 +346,11 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
       // allocate
       const size_t want =
           std::max(need, workspace_bytes(g, std::max(batch, kLibraryWorkspaceBatch), sp, waves));
-      if (int e = library_workspace(dev, stream, want, &ws, &ws_bytes)) return e;
-      std::lock_guard<std::mutex> lk(g_mu);
-      for (auto& w : g_dev[dev].ws)
-        if (w.ptr == ws)
-          if (int e = prepare_counters(ws, &w.zero_from, counter_start(g, batch, ws_bytes),
-                                       data_bytes(g, batch, sp, waves), stream))
-            return e;
+      if (int e = library_workspace(dev, stream, want, &ws)) return e;
     } else if (ws_bytes < need) {
       return fail(JACQ_KIVI_ENOMEM, "workspace of " + std::to_string(ws_bytes) +
                                          " bytes is smaller than the " + std::to_string(need) +
                                          " required");
-    } else if (is_scratch) {
-      std::lock_guard<std::mutex> lk(g_mu);
-      if (int e = prepare_counters(ws, &g_dev[dev].scratch_zero_from,
-                                   counter_start(g, batch, ws_bytes),
-                                   data_bytes(g, batch, sp, waves), stream))
-        return e;
     }
   }
   jacq::DecodeArgs a{};
@@ -392,7 +372,8 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
   a.out = O;
   a.out_stride = (int64_t)g.nh * g.hd;
   a.retained_pages = retained_pages;
-  fill_ws(a, g, batch, sp, waves, need > 0 ? ws : nullptr, ws_bytes);
+  a.status = ds.status_dev;
+  fill_ws(a, g, batch, sp, waves, need > 0 ? ws : nullptr);
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   profile_slot(ev);
   hipError_t e;
@@ -447,7 +428,9 @@ int run_append(const jacq_kivi_geometry& x, uint8_t* kc, jacq_half_t* ksc, jacq_
   return JACQ_KIVI_OK;
 }
 
-// CUDA_CHECK of the emitted v1 symbols: report and exit(1).
+// CUDA_CHECK of the emitted v1 symbols: report and exit(1).  A merge
+// time-out of an earlier decode is reported the same way by the next v1
+// decode on the device.
 void v1_check(int status, const char* where) {
   if (status == JACQ_KIVI_OK) return;
   if (status == JACQ_KIVI_EHIP) {
@@ -475,12 +458,36 @@ int jacq_kivi_init(void) {
   return current_device(&dev);
 }
 
-int jacq_kivi_profile_wave_stamps(uint64_t* buffer, int32_t capacity) {
-  if (buffer && capacity < 1) return fail(JACQ_KIVI_EINVAL, "capacity must be >= 1");
-  jacq::set_wave_stamps(buffer, buffer ? capacity : 0);
-  return JACQ_KIVI_OK;
+int jacq_kivi_decode_status(void* workspace, size_t workspace_bytes_, hipStream_t stream) {
+  int dev = 0;
+  if (int e = current_device(&dev)) return e;
+  if (hipStreamSynchronize(stream) != hipSuccess)
+    return fail(JACQ_KIVI_EHIP, "hipStreamSynchronize failed");
+  const DeviceInfo ds = device_state(dev);
+  if (*ds.status == 0) return JACQ_KIVI_OK;
+  // Reset: a timed-out merge left flags that its stream wavefronts set after
+  // it gave up; a graph replay (same epoch) would take them for its own.
+  // Every workspace the device's decodes may have used is cleared.
+  if (hipDeviceSynchronize() != hipSuccess) return fail(JACQ_KIVI_EHIP, "hipDeviceSynchronize failed");
+  std::vector<StreamWorkspace> all;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    all = g_dev[dev].ws;
+    all.insert(all.end(), g_dev[dev].retired.begin(), g_dev[dev].retired.end());
+    all.push_back({stream, g_dev[dev].scratch_ptr, kNoAllocScratchBytes});
+  }
+  if (workspace && workspace_bytes_) all.push_back({stream, workspace, workspace_bytes_});
+  for (const auto& w : all)
+    if (w.ptr && hipMemset(w.ptr, 0, w.bytes) != hipSuccess)
+      return fail(JACQ_KIVI_EHIP, "hipMemset(workspace) failed");
+  *ds.status = 0;
+  return fail(JACQ_KIVI_ETIMEOUT, "a split-K merge timed out since the last query; its "
+                                  "outputs were NaN; the workspaces are reset");
 }
 
+void jacq_kivi_test_force_merge_timeout(uint32_t microseconds) {
+  jacq::set_test_merge_timeout_us(microseconds);
+}
 
 int64_t jacq_kivi_max_seq_len(const jacq_kivi_geometry* geo) {
   if (check_geometry(geo) != JACQ_KIVI_OK) return -1;
@@ -567,7 +574,7 @@ int jacq_kivi_decode_noalloc(const jacq_kivi_geometry* geo, const jacq_half_t* Q
   return run_decode(*geo, Q, SEQ_LENS, -1, BLOCK_TABLES, geo->max_pages_per_seq, K_CODE_PAGES,
                     K_SCALE_PAGES, K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES,
                     K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, scr, batch, O, ds.scratch_ptr,
-                    kNoAllocScratchBytes, stream, -1, true);
+                    kNoAllocScratchBytes, stream);
 }
 
 int jacq_kivi_decode_sparse_retained(

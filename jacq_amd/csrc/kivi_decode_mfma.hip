@@ -37,7 +37,9 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cstdlib>
+#include <random>
 #include <type_traits>
 #include <utility>
 
@@ -725,38 +727,32 @@ __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, in
   return rt;
 }
 
-// ---- split-K merge, by the wavefront that completes a segment ----
+// ---- split-K merge, run by workgroups of the same launch ----
 //
-// A wavefront whose run cuts a (sequence, kv head) segment stores its
-// online-softmax partial with agent-scope stores (they reach the point of
+// The stream wavefronts fill every slot of the device, so the merge
+// workgroups (block ids past a.waves) start as stream wavefronts finish, on
+// the CUs the end of the launch leaves idle.  A wavefront that leaves a
+// partial stores it with agent-scope stores (they reach the point of
 // coherence of all XCDs without an L2 write-back), waits for them, and then
-// adds one to the segment's counter with an agent-scope atomic.  The pieces
-// of a segment follow from the static split, so every wavefront knows how
-// many there are: the one whose add completes the count reads the others'
-// partials with agent-scope loads, folds them in piece order (the result does
-// not depend on timing), writes O and sets the counter back to zero.  Nothing
-// waits on another wavefront, and every counter is zero again when a launch
-// ends, also for a graph replay.
+// stores the launch's 64-bit epoch in the partial's flag.  A merge wavefront
+// reads a partial only after it has read that epoch from the flag, with
+// agent-scope loads, and then clears the flag.  Every flag is therefore zero
+// when a launch starts -- also when a replayed graph repeats the epoch --
+// except in a fresh buffer, whose contents match a 64-bit epoch with
+// probability 2^-64; the workspace needs no reset.  The merge does not hold
+// anything a stream wavefront waits for, and there are at most half as many
+// merge workgroups as stream slots, so the stream wavefronts always run; a
+// merge wavefront that still waits after kMergeTimeoutTicks (s_memrealtime,
+// 100 MHz) writes NaN for its segments and ends, so the launch always drains.
+constexpr uint64_t kMergeTimeoutTicks = 100000000;  // 1 s
 
-static std::atomic<uint64_t*> g_stamps{nullptr};
-static std::atomic<int> g_stamp_cap{0};
-void set_wave_stamps(uint64_t* buf, int cap) {
-  g_stamp_cap.store(buf ? cap : 0, std::memory_order_relaxed);
-  g_stamps.store(buf, std::memory_order_relaxed);
-}
-
-// Profiling stamps of one workgroup (lane 0, plain vector stores).
-__device__ inline void write_stamp(const DecodeArgs& a, uint64_t t0, uint64_t units, int lane) {
-  const int b = blockIdx.x;
-  if (!a.stamps || b >= a.stamp_cap || lane != 0) return;
-  const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
-  const uint32_t hw = __builtin_amdgcn_s_getreg((4) | (0 << 6) | (31 << 11));     // HW_ID
-  const uint32_t xcc = __builtin_amdgcn_s_getreg((20) | (0 << 6) | (15 << 11));   // XCC_ID
-  uint64_t* p = a.stamps + 4 * (int64_t)b;
-  p[0] = t0;
-  p[1] = t1;
-  p[2] = (uint64_t)hw | ((uint64_t)xcc << 32);
-  p[3] = units;
+// Test-only (jacq_kivi_test_force_merge_timeout): when nonzero, every merge
+// waits for an epoch no stream wave stores and gives up after this many
+// s_memrealtime ticks, so a test can check from the host that a launch whose
+// merges time out still drains and reports it.  Zero in normal use.
+static std::atomic<uint64_t> g_test_merge_timeout_ticks{0};
+void set_test_merge_timeout_us(uint32_t us) {
+  g_test_merge_timeout_ticks.store((uint64_t)us * 100, std::memory_order_relaxed);  // 100 MHz
 }
 
 // Global unit index of (b, kv head 0): NKV times the units of the sequences before b.
@@ -803,52 +799,21 @@ __device__ inline void keep(floatx4& v) { asm volatile("" : "+v"(v)); }
 __device__ inline float lo_f(uint64_t v) { return __uint_as_float((uint32_t)v); }
 __device__ inline float hi_f(uint64_t v) { return __uint_as_float((uint32_t)(v >> 32)); }
 
-// The pieces of segment `seg`: wavefronts w0..w1 own units of it, and those
-// whose runs own at least one of its tiles left a piece (a run that starts
-// inside a residual tile owned by the previous run owns none of it).
-struct SegPieces {
-  int64_t w0, w1;
-  int64_t S0, S1;  // the segment's global unit range
-  int nq;          // its quantised groups
-  int count;       // non-empty pieces
-};
-
-__device__ inline bool piece_owns(int64_t w, const SegPieces& sp, int64_t TT, int64_t W) {
-  const int64_t x0 = max(run_begin(w, TT, W), sp.S0), x1 = min(run_begin(w + 1, TT, W), sp.S1);
-  return tile_at((int)(x0 - sp.S0), sp.nq) < tile_at((int)(x1 - sp.S0), sp.nq);
-}
-
-__device__ inline SegPieces segment_pieces(const KiviGeo& g, const DecodeArgs& a, int seg,
-                                           int64_t TT, int64_t W, int lane) {
-  const int NKV = g.nkv;
-  const int b = seg / NKV, h = seg - b * NKV;
-  int ov, n;
-  const int T = seq_tiles(g, a, b, &ov, &n);
-  SegPieces sp;
-  sp.nq = ov / kGroup;
-  const int units = sp.nq + kResidualUnits * (T - sp.nq);
-  sp.S0 = seq_start(g, a, b, lane) + (int64_t)h * units;
-  sp.S1 = sp.S0 + units;
-  sp.w0 = wave_of(sp.S0, TT, W);
-  sp.w1 = wave_of(sp.S1 - 1, TT, W);
-  sp.count = 0;
-  for (int64_t wb = sp.w0; wb <= sp.w1; wb += 64)
-    sp.count += __builtin_popcountll(__builtin_amdgcn_ballot_w64(
-        wb + lane <= sp.w1 && piece_owns(wb + lane, sp, TT, W)));
-  return sp;
-}
-
-// Log-sum-exp merge of a cut segment's partials (variants.rs:3548-3565):
-// M = max m_w, L = sum l_w e^(m_w - M), acc likewise, O = acc / max(L, 1e-30),
-// in the log2 domain of the decode loop.  Every piece has landed (the caller
-// completed the segment's count); they are folded in piece order.
+// Log-sum-exp merge of the partials of every (sequence, kv head) whose run was
+// cut (variants.rs:3548-3565): M = max m_w, L = sum l_w e^(m_w - M), acc
+// likewise, O = acc / max(L, 1e-30), in the log2 domain of the decode loop.
+// The pieces of a segment are recomputed from the same split the stream
+// wavefronts used; a segment with a single non-empty piece was written whole.
 template <int HD, bool PACK>
-__device__ void merge_segment(const KiviGeo& g, const DecodeArgs& a, int seg,
-                              const SegPieces& sp, int64_t TT, int64_t W, int lane) {
+__device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) {
   constexpr int K = (PACK ? 8 : 16) * HD / 256;  // float4 outputs per lane: G * HD <= 256 K
   constexpr int U = K <= 2 ? 8 : K > 4 ? 1 : 2;  // partials whose loads are in flight together
   const int G = g.gqa, NKV = g.nkv, n4 = G * HD / 4;
-  const int b = seg / NKV, h = seg - b * NKV;
+  const int64_t TT = stream_units(g, a, lane);
+  const int64_t W = stream_waves(TT, a.waves);
+  const int nseg = a.batch * NKV;
+  const uint64_t epoch = a.epoch + a.merge_skew, t_start = __builtin_amdgcn_s_memrealtime();
+  bool late = false;  // wave-uniform: the wait ran out
   int gi[K], d[K];
   bool on[K];
 #pragma unroll
@@ -858,81 +823,125 @@ __device__ void merge_segment(const KiviGeo& g, const DecodeArgs& a, int seg,
     gi[k] = 4 * e / HD;
     d[k] = 4 * e - gi[k] * HD;
   }
-  float M[K], Lsum[K];
-  floatx4 acc[K];
+  for (int seg = (int)blockIdx.x - a.waves; seg < nseg; seg += a.merge_wgs) {
+    const int b = seg / NKV, h = seg - b * NKV;
+    int ov, n;
+    const int T = seq_tiles(g, a, b, &ov, &n);
+    const int nq = ov / kGroup;
+    const int units = nq + kResidualUnits * (T - nq);
+    const int64_t S0 = seq_start(g, a, b, lane) + (int64_t)h * units, S1 = S0 + units;
+    const int64_t w0 = wave_of(S0, TT, W), w1 = wave_of(S1 - 1, TT, W);
+    // non-empty pieces: the runs that own at least one tile of the segment
+    auto owns = [&](int64_t w) {
+      const int64_t x0 = max(run_begin(w, TT, W), S0), x1 = min(run_begin(w + 1, TT, W), S1);
+      return tile_at((int)(x0 - S0), nq) < tile_at((int)(x1 - S0), nq);
+    };
+    int pieces = 0;
+    for (int64_t wb = w0; wb <= w1; wb += 64)
+      pieces += __builtin_popcountll(
+          __builtin_amdgcn_ballot_w64(wb + lane <= w1 && owns(wb + lane)));
+    if (pieces <= 1) continue;  // written whole by its wavefront
+
+    float M[K], Lsum[K];
+    floatx4 acc[K];
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    M[k] = -INFINITY;
-    Lsum[k] = 0.0f;
-    acc[k] = floatx4{0.f, 0.f, 0.f, 0.f};
-  }
-  for (int64_t wb = sp.w0; wb <= sp.w1; wb += 64) {
-    uint64_t todo = __builtin_amdgcn_ballot_w64(wb + lane <= sp.w1 &&
-                                                piece_owns(wb + lane, sp, TT, W));
-    while (todo) {
-      int64_t slot[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        slot[u] = -1;
-        if (todo) {
-          slot[u] = seg + wb + __builtin_ctzll(todo);
-          todo &= todo - 1;
+    for (int k = 0; k < K; ++k) {
+      M[k] = -INFINITY;
+      Lsum[k] = 0.0f;
+      acc[k] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int64_t wb = w0; wb <= w1 && !late; wb += 64) {
+      const int64_t wl = wb + lane;
+      const bool mine = wl <= w1 && owns(wl);
+      const uint64_t* flag = a.ws_flag + seg + wl;
+      uint64_t todo = __builtin_amdgcn_ballot_w64(mine);
+      // fold the partials in piece order (the result does not depend on
+      // timing), each run of them as soon as its flags show this launch's
+      // epoch: after the last one lands, only those behind it remain
+      while (todo) {
+        const uint64_t bit = 1ull << lane;
+        // one lane waits for the first piece in order ...
+        if (lane == __builtin_ctzll(todo)) {
+          while (ld_agent(flag) != epoch &&
+                 __builtin_amdgcn_s_memrealtime() - t_start <= a.merge_timeout)
+            __builtin_amdgcn_s_sleep(4);
         }
-      }
-      uint64_t ml[U][K];
-      floatx4 vv[U][K];
+        // ... then one round finds how many after it have landed too
+        const uint64_t landed =
+            __builtin_amdgcn_ballot_w64((todo & bit) && ld_agent(flag) == epoch);
+        // the ready prefix: pieces of todo below its first one not yet stored
+        const uint64_t waiting = todo & ~landed;
+        uint64_t ready = waiting ? todo & ((waiting & (0 - waiting)) - 1) : todo;
+        if (!ready) {  // the first piece's wait ran out
+          late = true;
+          break;
+        }
+        todo &= ~ready;
+        while (ready) {
+          int64_t slot[U];
+          uint64_t consumed = ready;  // after the loop below: the bits this round takes
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
+          for (int u = 0; u < U; ++u) {
+            slot[u] = -1;
+            if (ready) {
+              slot[u] = seg + wb + __builtin_ctzll(ready);
+              ready &= ready - 1;
+            }
+          }
+          consumed &= ~ready;
+          uint64_t ml[U][K];
+          floatx4 vv[U][K];
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-          ml[u][k] = 0xff800000u;  // (m, l) = (-inf, 0): folded with weight 0
-          vv[u][k] = floatx4{0.f, 0.f, 0.f, 0.f};
-          if (slot[u] >= 0 && on[k]) {
-            const int64_t p = slot[u] * G + gi[k];
-            ml[u][k] = ld_agent(a.ws_ml + 2 * p);
-            vv[u][k] = ld_agent4(a.ws_acc + p * HD + d[k]);
+          for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+              ml[u][k] = 0xff800000u;  // (m, l) = (-inf, 0): folded with weight 0
+              vv[u][k] = floatx4{0.f, 0.f, 0.f, 0.f};
+              if (slot[u] >= 0 && on[k]) {
+                const int64_t p = slot[u] * G + gi[k];
+                ml[u][k] = ld_agent(a.ws_ml + 2 * p);
+                vv[u][k] = ld_agent4(a.ws_acc + p * HD + d[k]);
+              }
+            }
+          }
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int k = 0; k < K; ++k) keep(vv[u][k]);
+          }
+          // read: clear the flags, so the next launch starts from zero even
+          // when it carries the same epoch (a replayed graph does)
+          if (consumed & bit)
+            __hip_atomic_store(a.ws_flag + seg + wl, 0ull, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+              const float m = lo_f(ml[u][k]), l = hi_f(ml[u][k]);
+              const float mn = fmaxf(M[k], m);
+              const float fo = __builtin_amdgcn_exp2f(M[k] - mn);
+              const float fn = __builtin_amdgcn_exp2f(m - mn);
+              const floatx4 v = vv[u][k];
+              acc[k] = acc[k] * fo + v * fn;
+              Lsum[k] = Lsum[k] * fo + l * fn;
+              M[k] = mn;
+            }
           }
         }
       }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          keep(vv[u][k]);
-          const float m = lo_f(ml[u][k]), l = hi_f(ml[u][k]);
-          const float mn = fmaxf(M[k], m);
-          const float fo = __builtin_amdgcn_exp2f(M[k] - mn);
-          const float fn = __builtin_amdgcn_exp2f(m - mn);
-          const floatx4 v = vv[u][k];
-          acc[k] = acc[k] * fo + v * fn;
-          Lsum[k] = Lsum[k] * fo + l * fn;
-          M[k] = mn;
-        }
-      }
     }
-  }
-  float* out = a.out + (int64_t)b * a.out_stride + (int64_t)h * G * HD;
+    float* out = a.out + (int64_t)b * a.out_stride + (int64_t)h * G * HD;
 #pragma unroll
-  for (int k = 0; k < K; ++k)
-    if (on[k]) *(floatx4*)(out + (int64_t)gi[k] * HD + d[k]) = acc[k] / fmaxf(Lsum[k], 1.0e-30f);
-}
-
-// A cut piece of segment `seg` has landed (its partial stores waited for):
-// count it; the wavefront that completes the count folds the segment.
-template <int HD, bool PACK>
-__device__ void piece_done(const KiviGeo& g, const DecodeArgs& a, int seg, int64_t TT, int64_t W,
-                           int lane) {
-  const SegPieces sp = segment_pieces(g, a, seg, TT, W, lane);
-  uint32_t old = 0;
-  if (lane == 0)
-    old = __hip_atomic_fetch_add(a.ws_count + seg, 1u, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-  old = __builtin_amdgcn_readfirstlane(old);
-  if ((int)old + 1 != sp.count) return;
-  merge_segment<HD, PACK>(g, a, seg, sp, TT, W, lane);
-  if (lane == 0)
-    __hip_atomic_store(a.ws_count + seg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int k = 0; k < K; ++k)
+      if (on[k])
+        *(floatx4*)(out + (int64_t)gi[k] * HD + d[k]) =
+            late ? floatx4{NAN, NAN, NAN, NAN} : acc[k] / fmaxf(Lsum[k], 1.0e-30f);
+  }
+  // a wait ran out: the host sees it in the device's status word
+  if (late && lane == 0 && a.status)
+    __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 template <int HD, int P, bool PACK>
@@ -945,7 +954,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   __shared__ __attribute__((aligned(16))) StageBuf<HD> ring[S];
 
   const int lane = threadIdx.x, c = lane & 15, j = lane >> 4;
-  const uint64_t t_start = a.stamps ? __builtin_amdgcn_s_memrealtime() : 0;
+  if ((int)blockIdx.x >= a.waves) {
+    merge_segments<HD, PACK>(g, a, lane);
+    return;
+  }
   const int G = g.gqa, NKV = g.nkv;
   // Up to 64 sequences, one length load per lane serves the stream's total,
   // the run's first sequence and that sequence's window: the first block-table
@@ -1017,9 +1029,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   int kvh = (int)((x0 - sp.start) / sp.units);
   int u = (int)((x0 - sp.start) % sp.units);  // unit offset inside the segment
   int64_t x = x0;
-  int cut_first = -1, cut_last = -1;  // segments this run leaves partials of
-  uint32_t n_segs = 0, n_res = 0;           // profiling: segments and fp16 tiles of the run
-  uint64_t t_first = 0;                     // profiling: first group in LDS
+  int64_t cut_first = -1, cut_last = -1;  // pieces this run leaves as partials
   while (x < x1) {
     const int b = sp.b, h = kvh;
     int ov = first_ov, n = first_n, T = first_T;
@@ -1037,7 +1047,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     // the run starts inside this segment's last residual tile, which the
     // previous wavefront owns: nothing here (no partial, no map entry)
     if (t_beg >= t_fin) continue;
-    ++n_segs;
 
     // ---- quantised groups: a ring of S LDS stages, S - 1 in flight ----
     const int tq_end = min(t_fin, ov / kGroup);
@@ -1097,7 +1106,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
         } else {
           wait_stages<L, S>(tq_end - 1 - i);
         }
-        if (a.stamps && t_first == 0) t_first = __builtin_amdgcn_s_memrealtime();
         const half8_t pa = qk_softmax<HD, P, PACK>(st, q, &ring[slot], lm, nb, sscale, lane);
         const VData vd = load_v<HD, P>(&ring[slot], lm);
         st.ob = mfma(pa, as_h8(vd.vz4), st.ob);  // sum_t P z_t
@@ -1141,7 +1149,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
       const uint32_t one2 = sum_col ? 0x3C003C00u : 0u;
       st.ob = mfma(pr, as_h8(u32x4{one2, one2, one2, one2}), st.ob);
       progress(kResidualUnits);
-      ++n_res;
     }
 
     // ---- segment output: O directly, or a partial for the merge workgroups ----
@@ -1210,27 +1217,24 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
                  ci == 0 ? lh[0] : ci == 1 ? lh[1] : ci == 2 ? lh[2] : lh[3]);
       }
       // only a run's first and last segments can be cut
-      (t_beg == 0 ? cut_last : cut_first) = b * NKV + h;
+      (t_beg == 0 ? cut_last : cut_first) = piece;
     }
   }
-  // count the cut pieces once their partials are complete at the point of
-  // coherence; the wavefront that completes a segment's count merges it
-  if (cut_first >= 0 || cut_last >= 0) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (cut_first >= 0) piece_done<HD, PACK>(g, a, cut_first, TT, W, lane);
-    if (cut_last >= 0) piece_done<HD, PACK>(g, a, cut_last, TT, W, lane);
+  // flags after the run: the partials are complete at the point of coherence
+  // before their flags are
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (lane == 0) {
+    if (cut_first >= 0)
+      __hip_atomic_store(a.ws_flag + cut_first, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (cut_last >= 0)
+      __hip_atomic_store(a.ws_flag + cut_last, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  write_stamp(a, t_start,
-              (uint64_t)min((int64_t)0xFFFF, x1 - x0) | ((uint64_t)min(n_segs, 255u) << 16) |
-                  ((uint64_t)min(n_res, 255u) << 24) |
-                  ((t_first ? t_first - t_start : 0) << 32),
-              lane);
 }
 
 template <int HD, int P>
 static void launch_one(const KiviGeo& g, const DecodeArgs& a, hipStream_t stream,
                        hipEvent_t start, hipEvent_t stop) {
-  const dim3 grid(a.waves);
+  const dim3 grid(a.waves + a.merge_wgs);
   if (g.gqa <= 8)
     hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, true>), grid, dim3(64), 0, stream,
                           start, stop, 0, g, a);
@@ -1241,10 +1245,27 @@ static void launch_one(const KiviGeo& g, const DecodeArgs& a, hipStream_t stream
 
 hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& args, int batch,
                               hipStream_t stream, const LaunchEvents& ev) {
-  (void)batch;
+  // One launch: the stream wavefronts, then the merge workgroups (at most
+  // half as many as stream slots, each taking segments in turn).  Every
+  // launch gets its own epoch, which marks the partials it stores.
+  // Epochs start from a random 64-bit value with the top bit set, so that
+  // leftover workspace contents (zeros, small integers, earlier epochs of
+  // other processes) are unlikely to match one.
+  static std::atomic<uint64_t> epochs{[] {
+    std::random_device rd;
+    const uint64_t t = (uint64_t)std::chrono::steady_clock::now().time_since_epoch().count();
+    const uint64_t r = ((uint64_t)rd() << 32) ^ rd() ^ (t * 0x9E3779B97F4A7C15ull);
+    return (r >> 2) | (1ull << 63);  // room for 2^62 launches before the top bit clears
+  }()};
   DecodeArgs a = args;
-  a.stamps = g_stamps.load(std::memory_order_relaxed);
-  a.stamp_cap = g_stamp_cap.load(std::memory_order_relaxed);
+  a.epoch = epochs.fetch_add(1, std::memory_order_relaxed);
+  a.merge_wgs = std::max(1, std::min(batch * g.nkv, a.waves / 2));
+  a.merge_timeout = kMergeTimeoutTicks;
+  a.merge_skew = 0;
+  if (const uint64_t t = g_test_merge_timeout_ticks.load(std::memory_order_relaxed)) {
+    a.merge_timeout = t;
+    a.merge_skew = 1;
+  }
   // Profiling only.  With main_end, the kernel's start and end are stamped by
   // the command processor (its own duration, as a kernel trace reads it);
   // that launch form delays the next kernel by a few microseconds, so without
@@ -1263,20 +1284,6 @@ hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& args, int batc
     launch_one<64, 32>(g, a, stream, s0, s1);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   return ev.end ? hipEventRecord(ev.end, stream) : hipSuccess;
-}
-
-__global__ void zero_words_kernel(uint32_t* p, size_t n) {
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (size_t)gridDim.x * blockDim.x)
-    p[i] = 0u;
-}
-
-hipError_t launch_zero(void* p, size_t bytes, hipStream_t stream) {
-  const size_t n = bytes / 4;
-  if (n == 0) return hipSuccess;
-  const unsigned blocks = (unsigned)std::min<size_t>(1024, (n + 255) / 256);
-  hipLaunchKernelGGL(zero_words_kernel, dim3(blocks), dim3(256), 0, stream, (uint32_t*)p, n);
-  return hipGetLastError();
 }
 
 // One resident wavefront per slot: the tile stream is cut into as many runs as

@@ -45,13 +45,16 @@ struct DecodeArgs {
   int64_t out_stride;
   float* ws_ml;   // [batch, NKV, max_splits, G, 2]  (m, l)
   float* ws_acc;  // [batch, NKV, max_splits, G, HD]
-  uint32_t* ws_count;  // matrix-core kernel: landed cut pieces per (sequence, kv head); zero between launches
+  uint64_t* ws_flag;  // matrix-core kernel: per partial slot, the epoch of the launch that stored it
   int max_splits;  // VALU kernel: split slots per (sequence, kv head)
   int batch;       // sequences (queries) in the call
   int waves;       // matrix-core kernel: wavefronts sharing the tile stream
+  int merge_wgs = 0;       // matrix-core kernel: merge workgroups after the stream wavefronts
+  uint64_t epoch = 0;      // matrix-core kernel: this launch's tag (set by the launcher)
+  uint64_t merge_timeout = 0;  // matrix-core kernel: s_memrealtime ticks a merge waits at most
+  uint64_t merge_skew = 0;     // matrix-core kernel: 0; 1 only in the forced-timeout test
   int retained_pages = -1;  // >= 0: sparse-retained window (compact block table)
-  uint64_t* stamps = nullptr;  // matrix-core kernel, profiling: 4 words per workgroup, or null
-  int stamp_cap = 0;           // workgroups the stamp buffer holds
+  uint32_t* status = nullptr;  // matrix-core kernel: set to 1 when a merge wait runs out
 };
 
 // Decode window of one sequence.  Dense: the split rule (decode_window).
@@ -72,9 +75,6 @@ __host__ __device__ inline void window_of(const KiviGeo& g, int retained_pages, 
   }
 }
 
-// Zero `bytes` (a multiple of 4) at `p` with a kernel on `stream` (no
-// memset node, so it may be captured into a graph).
-hipError_t launch_zero(void* p, size_t bytes, hipStream_t stream);
 hipError_t launch_append(const KiviGeo& g, const AppendArgs& a, int batch, hipStream_t stream);
 // `between`, when not null, is recorded on the stream after the main kernel
 // and before the split-K merge (profiling).
@@ -88,11 +88,10 @@ struct LaunchEvents {
 };
 hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
                               hipStream_t stream, const LaunchEvents& ev = LaunchEvents());
-// Profiling: while `buf` is not null, each later matrix-core decode's
-// workgroup b < cap writes {start, end} s_memrealtime ticks (100 MHz), its
-// HW_ID and XCC_ID, and the number of work units it processed, to
-// buf[4b .. 4b + 3] (words: start, end, hw_id | xcc_id << 32, units).
-void set_wave_stamps(uint64_t* buf, int cap);
+// Test-only: with us > 0 every later matrix-core decode's merge waits for an
+// epoch no wavefront stores and gives up after `us` microseconds; 0 restores
+// normal operation.
+void set_test_merge_timeout_us(uint32_t us);
 // wavefronts the matrix-core decode launches on a device with `cus` CUs:
 // as many as are resident at once
 int decode_stream_waves(const KiviGeo& g, int cus);

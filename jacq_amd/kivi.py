@@ -47,6 +47,13 @@ class KiviLaunchError(RuntimeError):
     pass
 
 
+class KiviMergeTimeout(KiviLaunchError):
+    """A split-K merge of an earlier decode timed out (JACQ_KIVI_ETIMEOUT)."""
+
+
+ETIMEOUT = 4
+
+
 class Geometry(ctypes.Structure):
     _fields_ = [
         ("num_heads", ctypes.c_int32),
@@ -139,8 +146,10 @@ def lib() -> ctypes.CDLL:
                                                _i32]
     L.jacq_kivi_plan_batched_write.restype = _i32
     L.jacq_kivi_init.restype = ctypes.c_int
-    L.jacq_kivi_profile_wave_stamps.argtypes = [_vp, _i32]
-    L.jacq_kivi_profile_wave_stamps.restype = ctypes.c_int
+    L.jacq_kivi_decode_status.argtypes = [_vp, ctypes.c_size_t, _vp]
+    L.jacq_kivi_decode_status.restype = ctypes.c_int
+    L.jacq_kivi_test_force_merge_timeout.argtypes = [ctypes.c_uint32]
+    L.jacq_kivi_test_force_merge_timeout.restype = None
     L.jacq_kivi_profile_start.argtypes = [_i32, _i32]
     L.jacq_kivi_profile_start.restype = ctypes.c_int
     L.jacq_kivi_profile_stop.argtypes = [ctypes.POINTER(ctypes.c_float),
@@ -154,6 +163,19 @@ def lib() -> ctypes.CDLL:
 
 def last_error() -> str:
     return lib().jacq_kivi_last_error().decode()
+
+
+def decode_status(workspace: torch.Tensor | None = None, device=None) -> None:
+    """Raise KiviMergeTimeout (after resetting the workspaces) if a decode's
+    split-K merge on the current device timed out since the last query."""
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    st = lib().jacq_kivi_decode_status(
+        _ptr(workspace), 0 if workspace is None else workspace.numel() * workspace.element_size(),
+        _stream(dev))
+    if st == ETIMEOUT:
+        raise KiviMergeTimeout(last_error())
+    if st != 0:
+        raise KiviLaunchError(last_error())
 
 
 def profile_start(max_calls: int, split: bool = True) -> None:
@@ -186,6 +208,8 @@ def profile_write_ms(cap: int = 4096):
 
 
 def _raise(rc: int) -> None:
+    if rc == ETIMEOUT:
+        raise KiviMergeTimeout(last_error())
     raise KiviLaunchError(last_error())
 
 

@@ -61,6 +61,7 @@ def test_noalloc_decode_equals_decode_twice(kivi):
         torch.cuda.synchronize()
         assert torch.equal(a.view(torch.int32), b.view(torch.int32)), f"batch {n}"
         assert_close(a.cpu().numpy(), ref[:n], f"noalloc batch {n}")
+    kivi.decode_status()
 
 
 def test_noalloc_rejects_batches_beyond_the_static_array(kivi):
