@@ -14,6 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libjacq_kivi.so")
+TORCH_LIB = os.path.join(HERE, "libjacq_kivi_torch.so")
 SOURCES = ["kivi_api.hip", "kivi_writer.hip", "kivi_decode.hip", "kivi_decode_mfma.hip"]
 ARCH = "gfx950"
 
@@ -83,5 +84,32 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+def build_torch_ops(verbose: bool = False) -> str:
+    """libjacq_kivi_torch.so: the torch custom ops (csrc/kivi_torch_ops.cpp)
+    over libjacq_kivi.so, found next to it through the $ORIGIN run path."""
+    import torch  # noqa: F401  (its headers and libraries)
+    from torch.utils import cpp_extension as ce
+
+    inc = [a for d in ce.include_paths(device_type="cuda") for a in ("-I", d)]
+    libdirs = [a for d in ce.library_paths(device_type="cuda") for a in ("-L", d)]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [hipcc(), "-O2", "-std=c++17", f"--offload-arch={ARCH}", "-fPIC", "-shared", "-Wall", "-Wno-unused-function",
+           "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "-I", os.path.join(ROOT, "include"), *inc,
+           os.path.join(CSRC, "kivi_torch_ops.cpp"), "-o", TORCH_LIB + ".tmp",
+           "-L", HERE, "-ljacq_kivi", "-Wl,-rpath,$ORIGIN", *libdirs,
+           "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip", "-ltorch", "-lamdhip64"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("hipcc failed building libjacq_kivi_torch.so")
+    os.replace(TORCH_LIB + ".tmp", TORCH_LIB)
+    return TORCH_LIB
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
+    print(build_torch_ops(verbose=True))
