@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--flush", choices=("read", "write"), default="read",
                     help="how the 512 MiB cache flush before each step touches its buffer")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--wave-stamps", default="", metavar="NPY",
+                    help="save per-workgroup start/end stamps of every timed decode of the "
+                         "first pass to NPY (jacq_kivi_profile_wave_stamps)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the workload, copy MIB MiB device-to-device a few times "
                          "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -134,6 +137,9 @@ def main() -> int:
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
 
     stream = torch.cuda.current_stream(dev)
+    STAMP_CAP = 8192  # workgroups per launch the stamp buffer holds
+    stamps = (torch.zeros((args.steps, STAMP_CAP, 4), dtype=torch.int64, device=dev)
+              if args.wave_stamps else None)
 
     def timed_pass(step0: int, split: bool):
         """warmup + steps of (flush, append, decode) from global step step0;
@@ -162,7 +168,12 @@ def main() -> int:
             e[0].record(stream)
             cache.append(nk[gi], nv[gi], bt, lens_before)
             e[1].record(stream)
+            if stamps is not None and not split and i >= args.warmup:
+                kivi.lib().jacq_kivi_profile_wave_stamps(
+                    kivi._ptr(stamps[i - args.warmup]), STAMP_CAP)
             cache.decode(qs[gi], lens_after, bt, out=out, workspace=workspace)
+            if stamps is not None:
+                kivi.lib().jacq_kivi_profile_wave_stamps(None, 0)
             e[2].record(stream)
             lens_before.add_(1)
             lens_after.add_(1)
@@ -178,6 +189,8 @@ def main() -> int:
     # pass 1 (the timed region of the contract): events only around each
     # decode, so the figure is the decode exactly as a caller runs it
     dec, _, wgpu, host, wall = timed_pass(0, split=False)
+    if stamps is not None:
+        np.save(args.wave_stamps, stamps.cpu().numpy())
     # pass 2: the same steps continued, the kernel's own start and end
     # stamped by the command processor (roofline)
     kern, _, _, _, _ = timed_pass(total_steps, split=True)

@@ -366,6 +366,14 @@ int32_t jacq_kivi_plan_batched_write(int32_t start_seq_len, int32_t num_new, int
  * records bracket the decode: kernel_ms then holds the whole decode and
  * merge_ms zero.  jacq_kivi_profile_write_ms then writes the per-call
  * milliseconds of the cache-write kernel recorded in the same window. */
+/* Profiling, additive, no counterpart in the reference: per-workgroup stamps
+ * of the following matrix-core decodes into `buffer` (device memory,
+ * capacity x 4 uint64): buffer[4b..4b+3] = {start, end} in s_memrealtime
+ * ticks (100 MHz), HW_ID | XCC_ID << 32, and for a stream workgroup its work
+ * units (bits 0-31) and the ticks until its first quantised group was in LDS
+ * (bits 32-63); 0 for the merge workgroups, which follow the stream ones.
+ * NULL turns it off. */
+int jacq_kivi_profile_wave_stamps(uint64_t* buffer, int32_t capacity);
 int jacq_kivi_profile_start(int32_t max_calls, int32_t split);
 int32_t jacq_kivi_profile_stop(float* kernel_ms, float* merge_ms, int32_t cap);
 int32_t jacq_kivi_profile_write_ms(float* ms, int32_t cap);

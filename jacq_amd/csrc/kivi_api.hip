@@ -520,6 +520,12 @@ size_t jacq_kivi_decode_workspace_size(const jacq_kivi_geometry* geo, int32_t ba
                          jacq::decode_stream_waves(g, device_state(dev).cus));
 }
 
+int jacq_kivi_profile_wave_stamps(uint64_t* buffer, int32_t capacity) {
+  if (buffer && capacity < 1) return fail(JACQ_KIVI_EINVAL, "capacity must be >= 1");
+  jacq::set_wave_stamps(buffer, buffer ? capacity : 0);
+  return JACQ_KIVI_OK;
+}
+
 int jacq_kivi_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q, const int32_t* SEQ_LENS,
                      const int32_t* BLOCK_TABLES, const uint8_t* K_CODE_PAGES,
                      const jacq_half_t* K_SCALE_PAGES, const jacq_half_t* K_ZERO_PAGES,

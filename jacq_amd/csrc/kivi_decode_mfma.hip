@@ -799,6 +799,28 @@ __device__ inline void keep(floatx4& v) { asm volatile("" : "+v"(v)); }
 __device__ inline float lo_f(uint64_t v) { return __uint_as_float((uint32_t)v); }
 __device__ inline float hi_f(uint64_t v) { return __uint_as_float((uint32_t)(v >> 32)); }
 
+// ---- profiling: per-workgroup stamps (jacq_kivi_profile_wave_stamps) ----
+static std::atomic<uint64_t*> g_stamps{nullptr};
+static std::atomic<int> g_stamp_cap{0};
+void set_wave_stamps(uint64_t* buf, int cap) {
+  g_stamp_cap.store(buf ? cap : 0, std::memory_order_relaxed);
+  g_stamps.store(buf, std::memory_order_relaxed);
+}
+// start and end (s_memrealtime, 100 MHz), HW_ID | XCC_ID << 32 and `info`,
+// written by lane 0 with plain vector stores
+__device__ inline void write_stamp(const DecodeArgs& a, uint64_t t0, uint64_t info, int lane) {
+  const int b = blockIdx.x;
+  if (!a.stamps || b >= a.stamp_cap || lane != 0) return;
+  const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+  const uint32_t hw = __builtin_amdgcn_s_getreg((4) | (0 << 6) | (31 << 11));    // HW_ID
+  const uint32_t xcc = __builtin_amdgcn_s_getreg((20) | (0 << 6) | (15 << 11));  // XCC_ID
+  uint64_t* p = a.stamps + 4 * (int64_t)b;
+  p[0] = t0;
+  p[1] = t1;
+  p[2] = (uint64_t)hw | ((uint64_t)xcc << 32);
+  p[3] = info;
+}
+
 // Log-sum-exp merge of the partials of every (sequence, kv head) whose run was
 // cut (variants.rs:3548-3565): M = max m_w, L = sum l_w e^(m_w - M), acc
 // likewise, O = acc / max(L, 1e-30), in the log2 domain of the decode loop.
@@ -954,8 +976,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   __shared__ __attribute__((aligned(16))) StageBuf<HD> ring[S];
 
   const int lane = threadIdx.x, c = lane & 15, j = lane >> 4;
+  const uint64_t t_start = a.stamps ? __builtin_amdgcn_s_memrealtime() : 0;
   if ((int)blockIdx.x >= a.waves) {
     merge_segments<HD, PACK>(g, a, lane);
+    write_stamp(a, t_start, 0, lane);
     return;
   }
   const int G = g.gqa, NKV = g.nkv;
@@ -1030,6 +1054,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   int u = (int)((x0 - sp.start) % sp.units);  // unit offset inside the segment
   int64_t x = x0;
   int64_t cut_first = -1, cut_last = -1;  // pieces this run leaves as partials
+  uint64_t t_first = 0;                   // profiling: first group in LDS
   while (x < x1) {
     const int b = sp.b, h = kvh;
     int ov = first_ov, n = first_n, T = first_T;
@@ -1106,6 +1131,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
         } else {
           wait_stages<L, S>(tq_end - 1 - i);
         }
+        if (a.stamps && t_first == 0) t_first = __builtin_amdgcn_s_memrealtime();
         const half8_t pa = qk_softmax<HD, P, PACK>(st, q, &ring[slot], lm, nb, sscale, lane);
         const VData vd = load_v<HD, P>(&ring[slot], lm);
         st.ob = mfma(pa, as_h8(vd.vz4), st.ob);  // sum_t P z_t
@@ -1229,6 +1255,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     if (cut_last >= 0)
       __hip_atomic_store(a.ws_flag + cut_last, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  // profiling: the run's units (bits 0-31) and the ticks to its first group (32-63)
+  write_stamp(a, t_start, (uint64_t)(x1 - x0) | ((t_first ? t_first - t_start : 0) << 32), lane);
 }
 
 template <int HD, int P>
@@ -1259,6 +1287,8 @@ hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& args, int batc
   }()};
   DecodeArgs a = args;
   a.epoch = epochs.fetch_add(1, std::memory_order_relaxed);
+  a.stamps = g_stamps.load(std::memory_order_relaxed);
+  a.stamp_cap = g_stamp_cap.load(std::memory_order_relaxed);
   a.merge_wgs = std::max(1, std::min(batch * g.nkv, a.waves / 2));
   a.merge_timeout = kMergeTimeoutTicks;
   a.merge_skew = 0;

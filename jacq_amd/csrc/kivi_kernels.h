@@ -49,6 +49,8 @@ struct DecodeArgs {
   int max_splits;  // VALU kernel: split slots per (sequence, kv head)
   int batch;       // sequences (queries) in the call
   int waves;       // matrix-core kernel: wavefronts sharing the tile stream
+  uint64_t* stamps = nullptr;  // matrix-core kernel, profiling: 4 words per workgroup, or null
+  int stamp_cap = 0;           // workgroups the stamp buffer holds
   int merge_wgs = 0;       // matrix-core kernel: merge workgroups after the stream wavefronts
   uint64_t epoch = 0;      // matrix-core kernel: this launch's tag (set by the launcher)
   uint64_t merge_timeout = 0;  // matrix-core kernel: s_memrealtime ticks a merge waits at most
@@ -86,6 +88,8 @@ hipError_t launch_decode(const KiviGeo& g, const DecodeArgs& a, int batch, hipSt
 struct LaunchEvents {
   hipEvent_t start = nullptr, main_end = nullptr, end = nullptr;
 };
+// Per-workgroup profiling stamps of the next matrix-core decodes (null: off).
+void set_wave_stamps(uint64_t* buf, int cap);
 hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& a, int batch,
                               hipStream_t stream, const LaunchEvents& ev = LaunchEvents());
 // Test-only: with us > 0 every later matrix-core decode's merge waits for an

@@ -150,6 +150,8 @@ def lib() -> ctypes.CDLL:
     L.jacq_kivi_decode_status.restype = ctypes.c_int
     L.jacq_kivi_test_force_merge_timeout.argtypes = [ctypes.c_uint32]
     L.jacq_kivi_test_force_merge_timeout.restype = None
+    L.jacq_kivi_profile_wave_stamps.argtypes = [_vp, _i32]
+    L.jacq_kivi_profile_wave_stamps.restype = ctypes.c_int
     L.jacq_kivi_profile_start.argtypes = [_i32, _i32]
     L.jacq_kivi_profile_start.restype = ctypes.c_int
     L.jacq_kivi_profile_stop.argtypes = [ctypes.POINTER(ctypes.c_float),

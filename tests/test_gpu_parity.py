@@ -596,3 +596,41 @@ def test_merge_timeout_exits_v1_symbols(kivi):
     assert "FIRST_DECODE_RETURNED" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]
     assert r.returncode == 1, r.stdout[-2000:] + r.stderr[-2000:]
     assert "jac_launch" in r.stderr and "timed out" in r.stderr, r.stderr[-2000:]
+
+
+def test_wave_stamps_cover_the_stream(kivi):
+    """The profiling hook (jacq_kivi_profile_wave_stamps): every stream
+    workgroup stamps an end after its start, and their units add up to the
+    stream's total (sum over sequences and kv heads of quantised groups plus
+    three units per fp16 residual tile)."""
+    from jacq_amd import cache_io
+    w = wl.WORKLOADS["qwen14b"].scaled(batch=4, ctx_lo=900)
+    lens = [900, 2000, 77, 3001]
+    st = State(w, lens=lens, seed=3)
+    st.build_oracle()
+    g = to_torch(st)
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, st.max_pages,
+                            st.num_pages)
+    cache = kivi.PagedKiviCache.from_tensors(geo, g)
+    q = torch.from_numpy(st.q).view(torch.float16).cuda()
+    cap = 8192
+    stamps = torch.zeros((cap, 4), dtype=torch.int64, device="cuda")
+    assert kivi.lib().jacq_kivi_profile_wave_stamps(kivi._ptr(stamps), cap) == 0
+    try:
+        out = cache.decode(q, torch.from_numpy(st.lens.astype(np.int32)).cuda(),
+                           torch.from_numpy(st.tables).cuda())
+        torch.cuda.synchronize()
+    finally:
+        assert kivi.lib().jacq_kivi_profile_wave_stamps(None, 0) == 0
+    assert_close(out.cpu().numpy(), st.decode_ref(), "decode with stamps")
+    s = stamps.cpu().numpy()
+    ran = s[:, 1] > 0
+    assert (s[ran, 1] >= s[ran, 0]).all()
+    units = s[:, 3] & 0xFFFFFFFF
+    expect = 0
+    for n in lens:
+        ov = cache_io.old_valid(geo, n)
+        tiles = max(1, -(-min(n, geo.max_seq_len()) // 32))
+        nq = ov // 32
+        expect += w.nkv * (nq + 3 * (tiles - nq))
+    assert int(units.sum()) == expect
