@@ -235,7 +235,8 @@ def main() -> int:
         "config": {
             "workload": f"{w.name}: {w.nh}q/{w.nkv}kv heads, head_dim {w.hd}, batch {B}, "
                         f"context U[{w.ctx_lo},{w.ctx_hi}], page {w.page}, group {w.group}, "
-                        f"residual {w.residual}, int4 KIVI K/V, fused cache write + decode",
+                        f"residual {w.residual}, int4 KIVI K/V, per step one cache write "
+                        f"launch then one decode launch (not fused)",
             "batch": B,
             "mean_context": float(np.mean(lens0)),
             "pages": num_pages,
