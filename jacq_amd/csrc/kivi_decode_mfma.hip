@@ -59,6 +59,13 @@ __device__ inline floatx4 mfma(half8_t a, half8_t b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// fp32 16x16x4: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16].  Its
+// i-th use over a tile takes element i of a lane's 16x16x32 f16 operand (k =
+// 8 (l / 16) + i), so eight of them cover the same 32 k.
+__device__ inline floatx4 mfma32(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 __device__ inline half8_t as_h8(u32x4 v) { return __builtin_bit_cast(half8_t, v); }
 __device__ inline u32x4 as_u4(half8_t v) { return __builtin_bit_cast(u32x4, v); }
 __device__ inline half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
@@ -84,14 +91,21 @@ struct Nibble {
 
 // 8 int4 codes of one dword (channel k at bits 4k..4k+3) -> A operand of one
 // k-step in the order [c0, c4, c1, c5, c2, c6, c3, c7]; odd channels carry a
-// factor 16 (their nibble sits in bits 4..7 of the mantissa).
+// factor 16 (their nibble sits in bits 4..7 of the mantissa).  The codes
+// enter as exact fp16 integers: (1024 + c) - 1024.  Leaving the 1024 in (and
+// subtracting 1024 sum B afterwards) cancels large fp32 sums; the masked bits
+// alone (c * 2^-24, subnormal) are exact too, but the matrix cores' sums of
+// subnormal products over operands of mixed magnitude are off by up to ~2^-16
+// relative -- either costs the scores about 1e-3 absolute, which large values
+// turn into output errors above 2e-3 + 1e-2 |O|.
 __device__ inline u32x4 unpack_codes(uint32_t x, const Nibble& nb) {
   const uint32_t x8 = x >> 8;
+  const half2_t m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
   u32x4 r;
-  r[0] = (x & nb.lo) | nb.magic;
-  r[1] = (x & nb.hi) | nb.magic;
-  r[2] = (x8 & nb.lo) | nb.magic;
-  r[3] = (x8 & nb.hi) | nb.magic;
+  r[0] = as_u(as_h2((x & nb.lo) | nb.magic) + m1024);
+  r[1] = as_u(as_h2((x & nb.hi) | nb.magic) + m1024);
+  r[2] = as_u(as_h2((x8 & nb.lo) | nb.magic) + m1024);
+  r[3] = as_u(as_h2((x8 & nb.hi) | nb.magic) + m1024);
   return r;
 }
 
@@ -206,6 +220,7 @@ struct StageBases {
 template <int HD, int P>
 __device__ inline StageBases stage_bases(const DecodeArgs& a, int nkv, int h, int lane) {
   using C = Cfg<HD, P>;
+  asm volatile("" : "+v"(lane));  // per segment, not hoisted into the whole run
   constexpr int KL = HD / 8;          // lanes per K scale (or zero) row
   constexpr int VL = 4 * C::HDG;      // lanes per V scale (or zero) block of 32 tokens
   StageBases sb;
@@ -387,12 +402,35 @@ __device__ inline void rescale(WaveState<HD>& st, float corr, int j) {
   for (int i = 0; i < 4; ++i) st.ob[i] *= ci[i];
 }
 
+// The fp32 P of a tile whose values need the exact PV steps, parked in LDS
+// in the k and v bytes of a ring slot whose contents are already in
+// registers or consumed (no DMA targets the slot until the next group): kept
+// in VGPRs from the softmax to the PV step it costs the common path's
+// schedule.  Element i of lane l (k = 8 (l / 16) + i) sits at float 64 i + l;
+// each lane reads back only what it wrote, so a one-wave workgroup needs no
+// barrier.  get() takes an opaque copy of the lane's offset, so every read is
+// a fresh ds_read, not a register kept live from the store.
+struct PStash {
+  float* base;
+  __device__ explicit PStash(uint8_t* bytes) : base((float*)bytes) {}
+  __device__ void put(const float (&p)[8]) const {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) base[64 * i + threadIdx.x] = p[i];
+  }
+  __device__ float get(int i) const {
+    int o = threadIdx.x;
+    asm volatile("" : "+v"(o));
+    return base[64 * i + o];
+  }
+};
+
 // Online-softmax update for raw scores s[tt][i] of tokens 8j + 4tt + i and
 // head c; the log2-domain score is fma(s, kscale, kbias).  Returns P as the
-// PV A operand.
+// fp16 PV A operand; with `precise` (wave-uniform) it also stores P in fp32
+// to `stash`.
 template <int HD>
 __device__ inline half8_t softmax_tile(WaveState<HD>& st, floatx4 s0, floatx4 s1, float kscale,
-                                       float kbias, int j) {
+                                       float kbias, int j, bool precise, const PStash& stash) {
   // max over the lane's 8 scores, then over the 4 lanes of head c (lanes
   // c, c+16, c+32, c+48) with the row-swap permutes (no LDS round trip)
   const float raw = max3f(max3f(s0[0], s0[1], s0[2]), max3f(s0[3], s1[0], s1[1]), max2f(s1[2], s1[3]));
@@ -412,6 +450,7 @@ __device__ inline half8_t softmax_tile(WaveState<HD>& st, floatx4 s0, floatx4 s1
     p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], kscale, off));
     p[4 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], kscale, off));
   }
+  if (__builtin_expect(precise, 0)) stash.put(p);
   half8_t pa;
 #pragma unroll
   for (int i = 0; i < 8; ++i) pa[i] = (_Float16)p[i];
@@ -460,6 +499,30 @@ __device__ inline uint64_t big_scales(const VData& d) {
   return __builtin_amdgcn_ballot_w64(big);  // nonzero: some lane holds a big scale
 }
 
+// The fp16 PV step rounds P and code * s to 11 bits and sums the zero-point
+// terms P z apart from the P code * s terms, so a token group's error scales
+// with |z| + 15 s (s >= 0), the larger of the two terms' magnitudes: up to
+// 2^-11 (|z| + 15 s) in the worst case.  Groups (and fp16 residual tiles,
+// whose values are exact: |V|) above kFastRange get the exact correction
+// (exact_fix); N(0,1) data, whose |z| + 15 s stays below ~11, never do.
+constexpr float kFastRange = 16.0f;
+
+// Some token group of the quantised group in `buf` has |z| + 15 s above
+// kFastRange.  The V scales and zeros are 16 HDG dwords each (two groups per
+// dword): each lane tests one of each, so the test costs two LDS reads and a
+// few packed operations, not a pass over the lane's redundant copies in VData.
+template <int HD>
+__device__ inline bool wide_group(const StageBuf<HD>* buf, int lane) {
+  constexpr int W = 16 * (HD / kGroup);  // dwords of V scales (and of zeros)
+  const uint8_t* vs = &buf->s[4 * HD];
+  const int o = 4 * (lane & (W - 1));
+  const half2_t sc = as_h2(*(const uint32_t*)(vs + o));
+  const half2_t z = as_h2(*(const uint32_t*)(vs + 4 * W + o) & 0x7FFF7FFFu);
+  const half2_t k15 = {(_Float16)15.0f, (_Float16)15.0f};
+  const half2_t r = __builtin_elementwise_fma(sc, k15, z);
+  return __builtin_amdgcn_ballot_w64((float)r[0] > kFastRange || (float)r[1] > kFastRange) != 0;
+}
+
 // PV of one group, dequantising the lane's V channels CPL*c + 2k (low
 // nibbles) and + 2k + 1 (high nibbles) for its 8 tokens.  x = 1024 + code is
 // exact in fp16, so code * s = fma(x, s, -1024 s) with one rounding; the high
@@ -468,10 +531,42 @@ __device__ inline uint64_t big_scales(const VData& d) {
 // x / 128 - 8 = code / 128 is formed first (exact), the products take a zero
 // addend and P carries the 128 back (powers of two: exact; P stays below
 // 2^15).  Both cases share one instruction stream and its registers.
+//
+// `precise` (wave-uniform; exact_fix_group): fp32 MFMAs (16x16x4) of the
+// fp32 P (from the stash `ps`) against code * s in fp32, which is exact (4 by
+// 11 significant bits), and against z for the zero-point sums (the row sums
+// in the sum columns); the caller adds none.  Only the fp32 products and
+// sums round, about 2^-24 relative; eight MFMAs cover what one f16 MFMA does.
 template <int HD>
-__device__ inline void pv_group(WaveState<HD>& st, half8_t pa, const VData& d, const Nibble& nb,
-                                uint64_t bigmask) {
+__device__ inline void pv_group(WaveState<HD>& st, half8_t ph, const VData& d,
+                                const Nibble& nb, uint64_t bigmask, bool precise,
+                                const PStash& ps) {
   constexpr int CPL = HD / 16;
+  if (__builtin_expect(precise, 0)) {
+    // fp32 P against fp32 values: code * s is exact in fp32 (4 x 11 bits), so
+    // the products carry fp32 rounding only
+    const half8_t zh = as_h8(d.vz4), sh = as_h8(d.vs4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.ob = mfma32(ps.get(i), (float)zh[i], st.ob);  // sum_t P z_t
+#pragma unroll
+    for (int k = 0; k < CPL / 2; ++k) {
+#pragma unroll
+      for (int nib = 0; nib < 2; ++nib) {  // low nibbles (channel 2k), then high (2k + 1)
+        floatx4& o = st.o[2 * k + nib];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t y = __builtin_amdgcn_perm(d.vc[2 * q + 1], d.vc[2 * q], nb.sel[k]);
+          const half2_t x = as_h2((y & (nib ? nb.hi : nb.lo)) | nb.magic);  // 1024 + c (16c)
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const float sc = (float)sh[2 * q + e] * (nib ? 0.0625f : 1.0f);
+            o = mfma32(ps.get(2 * q + e), ((float)x[e] - 1024.0f) * sc, o);
+          }
+        }
+      }
+    }
+    return;
+  }
   const half8_t sv = as_h8(d.vs4);
   // wave-uniform constants chosen by scalar selects on the ballot mask
   const bool big = bigmask != 0;
@@ -481,7 +576,7 @@ __device__ inline void pv_group(WaveState<HD>& st, half8_t pa, const VData& d, c
   const half8_t shi = sv * (_Float16)0.0625f;
   const u32x4 s_lo = d.vs4, s_hi = as_u4(shi);
   const u32x4 n_lo = as_u4(sv * f_n), n_hi = as_u4(shi * f_n);  // -1024 s (exact) or 0
-  const half8_t pv = pa * f_p;
+  const half8_t pv = ph * f_p;
   const half2_t r128_2 = {(_Float16)(1.0f / 128.0f), (_Float16)(1.0f / 128.0f)};
   const half2_t m8_2 = {(_Float16)-8.f, (_Float16)-8.f};
 #pragma unroll
@@ -514,27 +609,33 @@ __device__ inline void pv_group(WaveState<HD>& st, half8_t pa, const VData& d, c
 // Everything one (sequence, kv head) needs while its tiles are processed.
 template <int HD>
 struct SegCtx {
-  half8_t qn[HD / 32];  // B operand of Q, natural channel order (bias, residual tiles)
+  // B operand of Q in natural channel order (bias, residual tiles): the
+  // segment's Q rows sit in the wave's LDS block; the lane's 16 bytes of k-step
+  // ks at qn + 16 ks (zero rows for the columns past G).  In registers they
+  // would hold 16 VGPRs through every group.
+  const uint8_t* qn;
   half8_t qp[HD / 32];  // B operand of Q in the unpack order, odd channels / 16
+  __device__ half8_t n(int ks) const { return *(const half8_t*)(qn + 16 * ks); }
 };
 
 // QK^T of one quantised group (already in LDS) and its online-softmax update:
 // S^T = K Q^T with B = q*s as fp16 hi + lo (lo = fma(q, s, -hi)); returns P
-// as the PV A operand.
+// as the PV A operand (and stashes it in fp32 when `precise`).
+struct Scores {
+  floatx4 s0, s1;      // raw scores of tiles tt = 0, 1
+  float kscale, kbias;  // log2-domain score = fma(s, kscale, kbias)
+};
+
 template <int HD, int P, bool PACK>
-__device__ inline half8_t qk_softmax(WaveState<HD>& st, const SegCtx<HD>& q,
-                                     const StageBuf<HD>* buf, const LaneMap& lm, const Nibble& nb,
-                                     float sscale, int lane) {
+__device__ inline Scores qk_scores(const SegCtx<HD>& q, const StageBuf<HD>* buf,
+                                   const LaneMap& lm, const Nibble& nb, float sscale, int lane) {
   using C = Cfg<HD, P>;
   constexpr int KS = C::KS;
   const int j = lane >> 4;
-  const half8_t neg1024 = {(_Float16)-1024.f, (_Float16)-1024.f, (_Float16)-1024.f,
-                           (_Float16)-1024.f, (_Float16)-1024.f, (_Float16)-1024.f,
-                           (_Float16)-1024.f, (_Float16)-1024.f};
   typename C::kvec kc[2];
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) kc[tt] = *(const typename C::kvec*)&buf->k[lm.kread[tt]];
-  floatx4 bz = {0.f, 0.f, 0.f, 0.f}, bh = bz, bl = bz, s0 = bz, s1 = bz;
+  floatx4 bz = {0.f, 0.f, 0.f, 0.f}, s0 = bz, s1 = bz;
   if constexpr (PACK) {
     // G <= 8: columns 0-7 carry q*s (hi) of heads 0-7, columns 8-15 the
     // rounding remainder (lo) of the same heads, so one MFMA does both; a
@@ -550,25 +651,24 @@ __device__ inline half8_t qk_softmax(WaveState<HD>& st, const SegCtx<HD>& q,
       const half8_t sp = as_h8(perm_pairs(sv));
       const half8_t qs = q.qp[ks] * sp;
       const half8_t bq = __builtin_elementwise_fma(q.qp[ks], sp, lo_col ? -qs : half8_t(0));
-      bz = mfma(as_h8(zv), q.qn[ks], bz);  // sum_d z_d q_gd
-      bh = mfma(neg1024, bq, bh);           // -1024 sum_d B_gd (hi | lo)
+      bz = mfma(as_h8(zv), q.n(ks), bz);  // sum_d z_d q_gd
       s0 = mfma(as_h8(unpack_codes(kc[0][ks], nb)), bq, s0);
       s1 = mfma(as_h8(unpack_codes(kc[1][ks], nb)), bq, s1);
     }
-    // the bias is added before the hi/lo merge: a DPP add whose source is an
-    // MFMA result register is miscompiled (the DPP combiner reads the
-    // tuple's first register for every element), one on a VALU result is not
+    // the score scale is applied before the hi/lo merge: a DPP add whose
+    // source is an MFMA result register is miscompiled (the DPP combiner
+    // reads the tuple's first register for every element), one on a VALU
+    // result is not
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float t0 = s0[i] + bh[0], t1 = s1[i] + bh[0];
+      const float t0 = s0[i] * sscale, t1 = s1[i] * sscale;
       s0[i] = t0 + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
                        0, __builtin_bit_cast(int, t0), 0x128, 0xF, 0xF, false));
       s1[i] = t1 + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
                        0, __builtin_bit_cast(int, t1), 0x128, 0xF, 0xF, false));
     }
-    return softmax_tile<HD>(st, s0, s1, sscale, bz[0] * sscale, j);
+    return Scores{s0, s1, 1.0f, bz[0] * sscale};
   }
-  // three independent bias chains keep the dependent-MFMA latency short
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     const uint8_t* kp = &buf->s[2 * (j * (HD / 4) + 8 * ks)];
@@ -577,9 +677,7 @@ __device__ inline half8_t qk_softmax(WaveState<HD>& st, const SegCtx<HD>& q,
     const half8_t sp = as_h8(perm_pairs(sv));
     const half8_t qs = q.qp[ks] * sp;
     const half8_t ql = __builtin_elementwise_fma(q.qp[ks], sp, -qs);
-    bz = mfma(as_h8(zv), q.qn[ks], bz);  // sum_d z_d q_gd
-    bh = mfma(neg1024, qs, bh);           // -1024 sum_d B_gd
-    bl = mfma(neg1024, ql, bl);
+    bz = mfma(as_h8(zv), q.n(ks), bz);  // sum_d z_d q_gd
     const half8_t x0 = as_h8(unpack_codes(kc[0][ks], nb));
     const half8_t x1 = as_h8(unpack_codes(kc[1][ks], nb));
     s0 = mfma(x0, qs, s0);
@@ -588,8 +686,53 @@ __device__ inline half8_t qk_softmax(WaveState<HD>& st, const SegCtx<HD>& q,
     s1 = mfma(x1, ql, s1);
   }
   // every row of the bias tile holds the same per-head constant
-  const float bias = bz[0] + (bh[0] + bl[0]);
-  return softmax_tile<HD>(st, s0, s1, sscale, bias * sscale, j);
+  return Scores{s0, s1, sscale, bz[0] * sscale};
+}
+
+template <int HD, int P, bool PACK>
+__device__ inline half8_t qk_softmax(WaveState<HD>& st, const SegCtx<HD>& q,
+                                     const StageBuf<HD>* buf, const LaneMap& lm, const Nibble& nb,
+                                     float sscale, int lane) {
+  const Scores sc = qk_scores<HD, P, PACK>(q, buf, lm, nb, sscale, lane);
+  return softmax_tile<HD>(st, sc.s0, sc.s1, sc.kscale, sc.kbias, lane >> 4, false, PStash(nullptr));
+}
+
+// The exact correction of a quantised group whose fast PV step already ran
+// with P16 = pa: the same products with -P16 take that contribution out again
+// (fp16 products are exact in fp32, so this leaves only fp32 rounding), then
+// P in fp32 -- from the scores recomputed off the K codes still in the slot,
+// with the softmax state the fast step left -- meets fp32 values (pv_group's
+// exact branch), P parked in the slot's k and v bytes (V is in registers).
+template <int HD, int P, bool PACK>
+__device__ inline void exact_fix_group(WaveState<HD>& st, const SegCtx<HD>& q, StageBuf<HD>* buf,
+                                       const LaneMap& lm, const Nibble& nb, float sscale,
+                                       int lane, half8_t pa, const VData& vd) {
+  static_assert(sizeof(buf->k) + sizeof(buf->v) >= 64 * 8 * sizeof(float), "P stash");
+  // HD = 128: the stash fits in the k bytes and V is read again afterwards
+  // (kept in registers through the score step it would spill); HD = 64 keeps
+  // V and stashes over the k and v bytes
+  constexpr bool kReload = sizeof(buf->k) >= 64 * 8 * sizeof(float);
+  st.ob = mfma(-pa, as_h8(vd.vz4), st.ob);
+  pv_group<HD>(st, -pa, vd, nb, big_scales(vd), false, PStash(nullptr));
+  int ln = lane;
+  asm volatile("" : "+v"(ln));
+  const Scores sc = qk_scores<HD, P, PACK>(q, buf, lane_map<HD, P>(ln), nb, sscale, ln);
+  const float off = sc.kbias - st.m;
+  float p[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc.s0[i], sc.kscale, off));
+    p[4 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc.s1[i], sc.kscale, off));
+  }
+  const PStash ps(buf->k);  // after the score reads: LDS serves one wave in order
+  ps.put(p);
+  if constexpr (kReload) {
+    int l2 = lane;
+    asm volatile("" : "+v"(l2));
+    pv_group<HD>(st, pa, load_v<HD, P>(buf, lane_map<HD, P>(l2)), nb, 0, true, ps);
+  } else {
+    pv_group<HD>(st, pa, vd, nb, 0, true, ps);
+  }
 }
 
 // Tiles of one sequence: 32-token tiles of its decode window, at least one so
@@ -703,6 +846,9 @@ template <int HD>
 __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, int b, int h,
                                        int ov, int n, int tile, int lane) {
   constexpr int KS = HD / 32, CPL = HD / 16;
+  // lane offsets from an opaque copy of the lane id: hoisted out of the
+  // loops they would hold 64-bit registers through the whole run
+  asm volatile("" : "+v"(lane));
   const int c = lane & 15, j = lane >> 4;
   const uint16_t* kscr = a.k_scr + (int64_t)b * a.scr_stride + (int64_t)h * g.rs * HD;
   const uint16_t* vscr = a.v_scr + (int64_t)b * a.scr_stride + (int64_t)h * g.rs * HD;
@@ -974,6 +1120,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   constexpr int L = stage_loads<HD>(), S = stages<HD, PACK>();
   static_assert(S >= 2 && S <= 4, "wait_stages covers up to 3 stages in flight");
   __shared__ __attribute__((aligned(16))) StageBuf<HD> ring[S];
+  // Q rows of the current segment, one per MFMA column head (rows past G stay zero)
+  __shared__ __attribute__((aligned(16))) uint16_t qrows[(PACK ? 8 : 16) * HD];
 
   const int lane = threadIdx.x, c = lane & 15, j = lane >> 4;
   const uint64_t t_start = a.stamps ? __builtin_amdgcn_s_memrealtime() : 0;
@@ -1002,7 +1150,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   if (x0 >= x1) return;
 
   const Nibble nb;
-  const LaneMap lm = lane_map<HD, P>(lane);
   const bool sum_col = sum_lane<HD>(c);
   constexpr int C1 = kGroup / CPL - 1;  // a sum column (the first group's)
   // the ones block of every stage (the DMAs never write it)
@@ -1010,6 +1157,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
     for (int s_ = 0; s_ < S; ++s_) ((uint32_t*)ring[s_].ones)[lane] = 0x3C003C00u;
   }
+  // rows past G are read as zeros by the columns that carry no head
+  for (int i = lane; i < (int)(sizeof(qrows) / 16); i += 64) ((u32x4*)qrows)[i] = u32x4{0u, 0u, 0u, 0u};
   const float sscale = 1.4426950408889634f / __builtin_sqrtf((float)HD);  // log2(e)/sqrt(HD)
 
   // Issue arbitration favours the oldest of the waves sharing a SIMD, which left
@@ -1100,12 +1249,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     // ---- Q operands and softmax state (the loads overlap the first DMAs) ----
     SegCtx<HD> q;
     const uint16_t* qh = a.q + (int64_t)b * a.q_stride + (int64_t)h * G * HD;
+    const int hq = PACK ? (c & 7) : c;  // packed: columns c and c + 8 share head c
+    uint16_t* qrow = &qrows[hq * HD + j * (HD / 4)];
+    q.qn = (const uint8_t*)qrow;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      const int hq = PACK ? (c & 7) : c;  // packed: columns c and c + 8 share head c
-      if (hq < G) v = *(const u32x4*)(qh + hq * HD + j * (HD / 4) + 8 * ks);
-      q.qn[ks] = as_h8(v);
+      if (hq < G) {
+        v = *(const u32x4*)(qh + hq * HD + j * (HD / 4) + 8 * ks);
+        *(u32x4*)(qrow + 8 * ks) = v;  // the same words from columns c and c + 8
+      }
       const half8_t div = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)0.0625f, (_Float16)0.0625f,
                            (_Float16)1.0f, (_Float16)1.0f, (_Float16)0.0625f, (_Float16)0.0625f};
       q.qp[ks] = as_h8(perm_pairs(v)) * div;
@@ -1132,10 +1285,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
           wait_stages<L, S>(tq_end - 1 - i);
         }
         if (a.stamps && t_first == 0) t_first = __builtin_amdgcn_s_memrealtime();
-        const half8_t pa = qk_softmax<HD, P, PACK>(st, q, &ring[slot], lm, nb, sscale, lane);
+        // the lane map is recomputed per group from an opaque copy of the lane
+        // id: kept across the loop it would hold five registers
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const LaneMap lm = lane_map<HD, P>(ln);
         const VData vd = load_v<HD, P>(&ring[slot], lm);
+        const half8_t pa = qk_softmax<HD, P, PACK>(st, q, &ring[slot], lm, nb, sscale, lane);
         st.ob = mfma(pa, as_h8(vd.vz4), st.ob);  // sum_t P z_t
-        pv_group<HD>(st, pa, vd, nb, big_scales(vd));
+        pv_group<HD>(st, pa, vd, nb, big_scales(vd), false, PStash(nullptr));
+        // the range test comes last, so the steps above stay one block for
+        // the scheduler (a branch between them costs the common case ~15%)
+        if (__builtin_expect(wide_group<HD>(&ring[slot], lane), 0))
+          exact_fix_group<HD, P, PACK>(st, q, &ring[slot], lm, nb, sscale, lane, pa, vd);
         slot = slot == S - 1 ? 0 : slot + 1;
         progress(1);
       }
@@ -1150,18 +1312,29 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
       for (int tt = 0; tt < 2; ++tt) {
         sres[tt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) sres[tt] = mfma(as_h8(cur.kv[tt][ks]), q.qn[ks], sres[tt]);
+        for (int ks = 0; ks < KS; ++ks) sres[tt] = mfma(as_h8(cur.kv[tt][ks]), q.n(ks), sres[tt]);
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii)
           if (8 * j + 4 * tt + ii >= tn) sres[tt][ii] = -INFINITY;
       }
-      const half8_t pr = softmax_tile<HD>(st, sres[0], sres[1], sscale, 0.0f, j);
       // rows past the end carry P = 0 but must not carry NaN/Inf garbage
 #pragma unroll
       for (int r = 0; r < 8; ++r)
         if (8 * j + r >= tn) cur.vr[r] = typename ResTile<HD>::vrow_t(0u);
+      // P also goes to LDS in fp32 (slot 0 is idle: every stage DMA has
+      // landed), for the exact correction of values above kFastRange
+      const PStash ps(ring[0].k);
+      const half8_t prh = softmax_tile<HD>(st, sres[0], sres[1], sscale, 0.0f, j, true, ps);
+      half2_t vmax = {(_Float16)0.0f, (_Float16)0.0f};
 #pragma unroll
-      for (int nt = 0; nt < CPL; ++nt) {
+      for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int e = 0; e < (int)(sizeof(cur.vr[0]) / 4); ++e)
+          vmax = __builtin_elementwise_max(vmax, __builtin_elementwise_abs(as_h2(cur.vr[r][e])));
+      const bool wide = __builtin_amdgcn_ballot_w64((float)vmax[0] > kFastRange ||
+                                                    (float)vmax[1] > kFastRange) != 0;
+      // B operand of output columns nt: the tile rows' channels 16 nt + c
+      auto cols = [&](int nt) {
         u32x4 vb;
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
@@ -1169,11 +1342,32 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
           vb[qq] = (nt & 1) ? __builtin_amdgcn_perm(vb2, va, 0x07060302u)
                             : __builtin_amdgcn_perm(vb2, va, 0x05040100u);
         }
-        st.o[nt] = mfma(pr, as_h8(vb), st.o[nt]);
+        return as_h8(vb);
+      };
+#pragma unroll
+      for (int nt = 0; nt < CPL; ++nt) st.o[nt] = mfma(prh, cols(nt), st.o[nt]);
+      const uint32_t one2 = sum_col ? 0x3C003C00u : 0u;  // Sigma P into the sum columns
+      st.ob = mfma(prh, as_h8(u32x4{one2, one2, one2, one2}), st.ob);
+      if (__builtin_expect(wide, 0)) {
+        // exact correction: the same products with -P16 out, fp32 P against
+        // the (exact) fp16 values in
+#pragma unroll
+        for (int nt = 0; nt < CPL; ++nt) {
+          const half8_t vh = cols(nt);
+          st.o[nt] = mfma(-prh, vh, st.o[nt]);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) st.o[nt] = mfma32(ps.get(i), (float)vh[i], st.o[nt]);
+        }
+        // the column test is redone from an opaque lane id, not kept live
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const bool sc_ = sum_lane<HD>(ln & 15);
+        const uint32_t o2 = sc_ ? 0x3C003C00u : 0u;
+        st.ob = mfma(-prh, as_h8(u32x4{o2, o2, o2, o2}), st.ob);
+        const float one = sc_ ? 1.0f : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) st.ob = mfma32(ps.get(i), one, st.ob);
       }
-      // Sigma P into the sum columns (the fp16 tokens carry no zero point)
-      const uint32_t one2 = sum_col ? 0x3C003C00u : 0u;
-      st.ob = mfma(pr, as_h8(u32x4{one2, one2, one2, one2}), st.ob);
       progress(kResidualUnits);
     }
 

@@ -283,21 +283,37 @@ def test_seq_len_zero_and_clamp(kivi):
     assert_close(o_np[1], ref, "clamped")
 
 
-def test_decode_extreme_value_scales(kivi):
-    """V tokens whose 32-channel ranges reach ~1e4: V scales >= 64 (where
-    -1024*s leaves fp16) and code*s products beyond 65504 take the scaled
-    path of the PV step.  Results stay finite and within the tolerance plus
-    the rounding of the fp16 MFMA operands (P, and code*s, each carry up to
-    2^-11 relative), 2^-10 * sum_t P_t (|code*s|_t + |zero|_t) -- with values
-    this large and outputs that cancel, that term exceeds 1e-2 * |O| (the
-    reference dequantises in fp32)."""
-    w = wl.WORKLOADS["qwen14b"]
-    st = State(w, lens=[700, 333], seed=5)
-    rng = np.random.default_rng(55)
+_EXTREME_GEOS = {
+    "hd128_g5": wl.WORKLOADS["qwen14b"],  # packed hi/lo QK columns, page 16
+    "hd64_g10_p32": wl.Workload("x64", 40, 4, 64, 1, 4096, 4096, page=32, residual=128,
+                                outliers=4, outlier_scale=10.0, seed=11),
+    "hd128_g16_p32": wl.Workload("x128", 32, 2, 128, 1, 4096, 4096, page=32, residual=128,
+                                 outliers=4, outlier_scale=10.0, seed=12),
+}
+
+
+@pytest.mark.parametrize("geo_id", list(_EXTREME_GEOS))
+@pytest.mark.parametrize("mults,seed,frac", [([100.0, 3000.0, 9000.0], 5, 0.3), ([30.0], 8, 0.3),
+                                              ([3000.0], 7, 0.3), ([300.0], 9, 0.01)],
+                         ids=["to9000", "x30", "x3000", "sparse_x300"])
+def test_decode_extreme_value_scales(kivi, mults, seed, frac, geo_id):
+    """V tokens scaled so that values reach 1e2..1e4 (V scales >= 64, where
+    -1024*s leaves fp16, and code*s beyond 65504): the results stay within
+    north_star's tolerance, max-abs 2e-3 / rel 1e-2 of the float64 two-pass
+    reference.  Such groups and residual tiles get the exact correction (fp32
+    P against fp32 values) after the fp16 PV step, without which the fp16
+    rounding of large, cancelling terms exceeds the bound by up to 64x; the
+    scores use exact integer K codes, whose matrix-core sums stay within a few
+    fp32 ulps (an offset code, or subnormal codes, cost up to 3.6x the bound).
+    sparse_x300 scales 1% of the tokens: most groups stay on the fp16 path and
+    a few are corrected in the same segment."""
+    w = _EXTREME_GEOS[geo_id]
+    st = State(w, lens=[700, 333], seed=seed)
+    rng = np.random.default_rng(50 + seed)
     for b in range(st.batch):
         v = st.v_hist[b].view(np.float16).astype(np.float32)
-        pick = rng.random(v.shape[0]) < 0.3
-        v[pick] *= rng.choice([100.0, 3000.0, 9000.0], size=(int(pick.sum()), 1, 1))
+        pick = rng.random(v.shape[0]) < frac
+        v[pick] *= rng.choice(mults, size=(int(pick.sum()), 1, 1))
         st.v_hist[b] = np.clip(v, -65000, 65000).astype(np.float16).view(np.uint16)
     st.build_oracle()
     g = to_torch(st)
@@ -309,16 +325,9 @@ def test_decode_extreme_value_scales(kivi):
     torch.cuda.synchronize()
     ref = st.decode_ref()
     got = out.cpu().numpy()
-    assert np.abs(ref).max() > 1000.0  # the case reaches the large-scale regime
+    assert np.abs(ref).max() > min(mults) / 100.0  # the large-value regime
     assert np.isfinite(got).all()
-    from tests import kivi_numpy_ref as nref
-    for b in range(st.batch):
-        K, (cs, z) = nref.dequant_sequence(st.cache, b, st.tables[b], int(st.lens[b]),
-                                           value_parts=True)
-        mag = nref.attention(st.q[b], K, np.abs(cs) + np.abs(z))  # sum_t P_t (|cs| + |z|)
-        bound = 2e-3 + 1e-2 * np.abs(ref[b]) + 2.0 ** -10 * mag
-        err = np.abs(got[b] - ref[b])
-        assert (err <= bound).all(), f"seq {b}: worst excess {(err - bound).max():.3e}"
+    assert_close(got, ref, f"values scaled by {mults}")
 
 
 def test_caller_workspace_needs_no_initial_contents(kivi):
