@@ -484,8 +484,14 @@ __device__ inline VData load_v(const StageBuf<HD>* buf, const LaneMap& lm) {
   for (int e = 0; e < 4; ++e) {  // pair q = e: tokens two rows apart
     const uint8_t* p0 = vp + 8 * HDG * e;
     const uint8_t* z0 = zp + 8 * HDG * e;
-    d.vs4[e] = (uint32_t)*(const uint16_t*)p0 | ((uint32_t)*(const uint16_t*)(p0 + 4 * HDG) << 16);
-    d.vz4[e] = (uint32_t)*(const uint16_t*)z0 | ((uint32_t)*(const uint16_t*)(z0 + 4 * HDG) << 16);
+    // element inserts: ds_read_u16_d16 / _d16_hi fill the halves in place
+    half2_t sv, zv;
+    sv[0] = *(const _Float16*)p0;
+    sv[1] = *(const _Float16*)(p0 + 4 * HDG);
+    zv[0] = *(const _Float16*)z0;
+    zv[1] = *(const _Float16*)(z0 + 4 * HDG);
+    d.vs4[e] = as_u(sv);
+    d.vz4[e] = as_u(zv);
   }
   return d;
 }
@@ -527,10 +533,11 @@ __device__ inline bool wide_group(const StageBuf<HD>* buf, int lane) {
 // nibbles) and + 2k + 1 (high nibbles) for its 8 tokens.  x = 1024 + code is
 // exact in fp16, so code * s = fma(x, s, -1024 s) with one rounding; the high
 // nibble carries 16x and uses s / 16.  When some |s| >= 64 (`big`,
-// wave-uniform) -1024 s and even code * s can leave the fp16 range: then
-// x / 128 - 8 = code / 128 is formed first (exact), the products take a zero
-// addend and P carries the 128 back (powers of two: exact; P stays below
-// 2^15).  Both cases share one instruction stream and its registers.
+// wave-uniform) -1024 s and even code * s can leave the fp16 range.  Such a
+// group always takes the exact correction (15 s > kFastRange), so the fp16
+// step only has to stay finite and be repeatable: by scalar selects, with no
+// branch to split the loop body, it contributes exactly zero (scales and
+// offsets 0: fma(1024 + c, 0, 0)).
 //
 // `precise` (wave-uniform; exact_fix_group): fp32 MFMAs (16x16x4) of the
 // fp32 P (from the stash `ps`) against code * s in fp32, which is exact (4 by
@@ -570,30 +577,23 @@ __device__ inline void pv_group(WaveState<HD>& st, half8_t ph, const VData& d,
   const half8_t sv = as_h8(d.vs4);
   // wave-uniform constants chosen by scalar selects on the ballot mask
   const bool big = bigmask != 0;
+  const uint32_t fs2 = __builtin_amdgcn_readfirstlane(big ? 0u : 0x3C003C00u);   // 0 or 1
+  const uint32_t fh2 = __builtin_amdgcn_readfirstlane(big ? 0u : 0x2C002C00u);   // 0 or 1/16
   const uint32_t fn2 = __builtin_amdgcn_readfirstlane(big ? 0u : 0xE400E400u);   // 0 or -1024
-  const uint32_t fp2 = __builtin_amdgcn_readfirstlane(big ? 0x58005800u : 0x3C003C00u);  // 128 or 1
-  const _Float16 f_n = as_h2(fn2)[0], f_p = as_h2(fp2)[0];
-  const half8_t shi = sv * (_Float16)0.0625f;
-  const u32x4 s_lo = d.vs4, s_hi = as_u4(shi);
-  const u32x4 n_lo = as_u4(sv * f_n), n_hi = as_u4(shi * f_n);  // -1024 s (exact) or 0
-  const half8_t pv = ph * f_p;
-  const half2_t r128_2 = {(_Float16)(1.0f / 128.0f), (_Float16)(1.0f / 128.0f)};
-  const half2_t m8_2 = {(_Float16)-8.f, (_Float16)-8.f};
+  const _Float16 f_s = as_h2(fs2)[0], f_h = as_h2(fh2)[0], f_n = as_h2(fn2)[0];
+  const half8_t slo = sv * f_s, shi = sv * f_h;  // s, s / 16 (exact) or 0
+  const u32x4 s_lo = as_u4(slo), s_hi = as_u4(shi);
+  const u32x4 n_lo = as_u4(slo * f_n), n_hi = as_u4(shi * f_n);  // -1024 s (exact) or 0
+  const half8_t pv = ph;
+  const uint32_t magic = nb.magic;
 #pragma unroll
   for (int k = 0; k < CPL / 2; ++k) {
     uint32_t xl[4], xh[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const uint32_t y = __builtin_amdgcn_perm(d.vc[2 * q + 1], d.vc[2 * q], nb.sel[k]);
-      xl[q] = (y & nb.lo) | nb.magic;  // (1024 + c, 1024 + c')
-      xh[q] = (y & nb.hi) | nb.magic;  // (1024 + 16c, 1024 + 16c')
-    }
-    if (__builtin_expect(big, 0)) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        xl[q] = as_u(__builtin_elementwise_fma(as_h2(xl[q]), r128_2, m8_2));  // code / 128
-        xh[q] = as_u(__builtin_elementwise_fma(as_h2(xh[q]), r128_2, m8_2));  // code / 8
-      }
+      xl[q] = (y & nb.lo) | magic;  // (1024 + c, 1024 + c')
+      xh[q] = (y & nb.hi) | magic;  // (1024 + 16c, 1024 + 16c')
     }
     u32x4 lo, hi;
 #pragma unroll
@@ -1271,6 +1271,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
 
     const int r_beg = max(t_beg, ov / kGroup);  // first fp16 residual tile
     if (t_beg < tq_end) {
+      const LaneMap lm = lane_map<HD, P>(lane);
       int slot = 0;
       for (int i = t_beg; i < tq_end; ++i) {
         const int ahead = slot == 0 ? S - 1 : slot - 1;  // (slot + S - 1) % S
@@ -1285,11 +1286,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
           wait_stages<L, S>(tq_end - 1 - i);
         }
         if (a.stamps && t_first == 0) t_first = __builtin_amdgcn_s_memrealtime();
-        // the lane map is recomputed per group from an opaque copy of the lane
-        // id: kept across the loop it would hold five registers
-        int ln = lane;
-        asm volatile("" : "+v"(ln));
-        const LaneMap lm = lane_map<HD, P>(ln);
         const VData vd = load_v<HD, P>(&ring[slot], lm);
         const half8_t pa = qk_softmax<HD, P, PACK>(st, q, &ring[slot], lm, nb, sscale, lane);
         st.ob = mfma(pa, as_h8(vd.vz4), st.ob);  // sum_t P z_t
