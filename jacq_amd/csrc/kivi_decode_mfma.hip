@@ -1121,7 +1121,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   static_assert(S >= 2 && S <= 4, "wait_stages covers up to 3 stages in flight");
   __shared__ __attribute__((aligned(16))) StageBuf<HD> ring[S];
   // Q rows of the current segment, one per MFMA column head (rows past G stay zero)
-  __shared__ __attribute__((aligned(16))) uint16_t qrows[(PACK ? 8 : 16) * HD];
+  // Q rows padded by 16 bytes: at a 2 HD-byte stride (a multiple of the 256
+  // bytes the LDS banks span) the rows' k-step reads would all hit the same
+  // banks, an 8-way conflict on every read
+  constexpr int QROW = HD + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t qrows[(PACK ? 8 : 16) * QROW];
 
   const int lane = threadIdx.x, c = lane & 15, j = lane >> 4;
   const uint64_t t_start = a.stamps ? __builtin_amdgcn_s_memrealtime() : 0;
@@ -1250,7 +1254,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     SegCtx<HD> q;
     const uint16_t* qh = a.q + (int64_t)b * a.q_stride + (int64_t)h * G * HD;
     const int hq = PACK ? (c & 7) : c;  // packed: columns c and c + 8 share head c
-    uint16_t* qrow = &qrows[hq * HD + j * (HD / 4)];
+    uint16_t* qrow = &qrows[hq * QROW + j * (HD / 4)];
     q.qn = (const uint8_t*)qrow;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
