@@ -1253,14 +1253,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     // ---- Q operands and softmax state (the loads overlap the first DMAs) ----
     SegCtx<HD> q;
     const uint16_t* qh = a.q + (int64_t)b * a.q_stride + (int64_t)h * G * HD;
-    const int hq = PACK ? (c & 7) : c;  // packed: columns c and c + 8 share head c
-    uint16_t* qrow = &qrows[hq * QROW + j * (HD / 4)];
+    // lane offsets from an opaque lane id (hoisted out of the segment loop,
+    // they would hold 64-bit registers through the whole run)
+    int lq = lane;
+    asm volatile("" : "+v"(lq));
+    const int hq = PACK ? (lq & 7) : (lq & 15);  // packed: columns c and c + 8 share head c
+    const int jq = lq >> 4;
+    uint16_t* qrow = &qrows[hq * QROW + jq * (HD / 4)];
     q.qn = (const uint8_t*)qrow;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       u32x4 v = {0u, 0u, 0u, 0u};
       if (hq < G) {
-        v = *(const u32x4*)(qh + hq * HD + j * (HD / 4) + 8 * ks);
+        v = *(const u32x4*)(qh + hq * HD + jq * (HD / 4) + 8 * ks);
         *(u32x4*)(qrow + 8 * ks) = v;  // the same words from columns c and c + 8
       }
       const half8_t div = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)0.0625f, (_Float16)0.0625f,
@@ -1344,29 +1349,28 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
         }
         return as_h8(vb);
       };
-#pragma unroll
-      for (int nt = 0; nt < CPL; ++nt) st.o[nt] = mfma(prh, cols(nt), st.o[nt]);
-      const uint32_t one2 = sum_col ? 0x3C003C00u : 0u;  // Sigma P into the sum columns
-      st.ob = mfma(prh, as_h8(u32x4{one2, one2, one2, one2}), st.ob);
-      if (__builtin_expect(wide, 0)) {
-        // exact correction: the same products with -P16 out, fp32 P against
-        // the (exact) fp16 values in
+      // A residual tile (a few per segment, not the hot loop) takes one
+      // arithmetic or the other, chosen before its PV step: a correction
+      // after the fp16 step would turn an infinite value into inf - inf.
+      if (__builtin_expect(wide, 0)) {  // fp32 P against the (exact) fp16 values
 #pragma unroll
         for (int nt = 0; nt < CPL; ++nt) {
           const half8_t vh = cols(nt);
-          st.o[nt] = mfma(-prh, vh, st.o[nt]);
 #pragma unroll
           for (int i = 0; i < 8; ++i) st.o[nt] = mfma32(ps.get(i), (float)vh[i], st.o[nt]);
         }
-        // the column test is redone from an opaque lane id, not kept live
+        // Sigma P into the sum columns; the column test is redone from an
+        // opaque lane id, not kept live
         int ln = lane;
         asm volatile("" : "+v"(ln));
-        const bool sc_ = sum_lane<HD>(ln & 15);
-        const uint32_t o2 = sc_ ? 0x3C003C00u : 0u;
-        st.ob = mfma(-prh, as_h8(u32x4{o2, o2, o2, o2}), st.ob);
-        const float one = sc_ ? 1.0f : 0.0f;
+        const float one = sum_lane<HD>(ln & 15) ? 1.0f : 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) st.ob = mfma32(ps.get(i), one, st.ob);
+      } else {
+#pragma unroll
+        for (int nt = 0; nt < CPL; ++nt) st.o[nt] = mfma(prh, cols(nt), st.o[nt]);
+        const uint32_t one2 = sum_col ? 0x3C003C00u : 0u;  // Sigma P into the sum columns
+        st.ob = mfma(prh, as_h8(u32x4{one2, one2, one2, one2}), st.ob);
       }
       progress(kResidualUnits);
     }

@@ -330,6 +330,43 @@ def test_decode_extreme_value_scales(kivi, mults, seed, frac, geo_id):
     assert_close(got, ref, f"values scaled by {mults}")
 
 
+@pytest.mark.parametrize("geo_id", ["hd128_g5", "hd64_g10_p32"])
+def test_decode_nonfinite_values(kivi, geo_id):
+    """+inf in V in a quantised token, -inf in an fp16 residual token.  The
+    reference dequantises the first with an infinite scale, 0 * inf = NaN for
+    its whole 32-channel group: every head of that kv head reads NaN there.
+    The second stays -inf in its channel.  The kernel gives the float64
+    reference's NaN and infinity positions (the infinite scale takes the exact
+    correction; the residual tile takes the fp32 path before its PV step, since
+    taking an fp16 step's -inf out again would leave inf - inf), and every
+    finite output stays within the tolerance."""
+    w = _EXTREME_GEOS[geo_id]
+    st = State(w, lens=[700, 333], seed=21)
+    v = st.v_hist[0].view(np.float16).astype(np.float32)
+    v[100, 1, 3] = np.inf       # quantised group of tokens 96..127, kv head 1
+    v[650, 0, 40] = -np.inf     # residual window of a 700-token sequence, kv head 0
+    st.v_hist[0] = v.astype(np.float16).view(np.uint16)
+    st.build_oracle()
+    g = to_torch(st)
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, st.max_pages, st.num_pages)
+    cache = kivi.PagedKiviCache.from_tensors(geo, g)
+    q = torch.from_numpy(st.q).view(torch.float16).cuda()
+    out = cache.decode(q, torch.from_numpy(st.lens.astype(np.int32)).cuda(),
+                       torch.from_numpy(st.tables).cuda())
+    torch.cuda.synchronize()
+    with np.errstate(invalid="ignore"):
+        ref = st.decode_ref()
+    got = out.cpu().numpy()
+    G = w.nh // w.nkv
+    assert np.isnan(ref[0, G:2 * G, 0:32]).all()
+    assert (ref[0, 0:G, 40] == -np.inf).all()
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), "NaN positions differ"
+    assert np.array_equal(np.isinf(got), np.isinf(ref)), "infinity positions differ"
+    assert (np.sign(got[np.isinf(ref)]) == np.sign(ref[np.isinf(ref)])).all()
+    fin = np.isfinite(ref)
+    assert_close(got[fin], ref[fin], f"finite outputs beside the non-finite groups ({geo_id})")
+
+
 def test_caller_workspace_needs_no_initial_contents(kivi):
     """A caller workspace filled with random bytes, then reused by a second
     call with other queries, decodes to the same bits as the library's own
