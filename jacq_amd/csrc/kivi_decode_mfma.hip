@@ -484,7 +484,8 @@ __device__ inline VData load_v(const StageBuf<HD>* buf, const LaneMap& lm) {
   for (int e = 0; e < 4; ++e) {  // pair q = e: tokens two rows apart
     const uint8_t* p0 = vp + 8 * HDG * e;
     const uint8_t* z0 = zp + 8 * HDG * e;
-    // element inserts: ds_read_u16_d16 / _d16_hi fill the halves in place
+    // element inserts: the compiler pairs the two halves with one v_perm,
+    // not a shift and an or
     half2_t sv, zv;
     sv[0] = *(const _Float16*)p0;
     sv[1] = *(const _Float16*)(p0 + 4 * HDG);
@@ -508,9 +509,10 @@ __device__ inline uint64_t big_scales(const VData& d) {
 // The fp16 PV step rounds P and code * s to 11 bits and sums the zero-point
 // terms P z apart from the P code * s terms, so a token group's error scales
 // with |z| + 15 s (s >= 0), the larger of the two terms' magnitudes: up to
-// 2^-11 (|z| + 15 s) in the worst case.  Groups (and fp16 residual tiles,
-// whose values are exact: |V|) above kFastRange get the exact correction
-// (exact_fix); N(0,1) data, whose |z| + 15 s stays below ~11, never do.
+// 2^-11 (|z| + 15 s) in the worst case.  Groups above kFastRange get the
+// exact correction (exact_fix_group), fp16 residual tiles with some |V| above
+// it (their values are exact) the fp32 path; N(0,1) data, whose |z| + 15 s
+// stays below ~11, never do.
 constexpr float kFastRange = 16.0f;
 
 // Some token group of the quantised group in `buf` has |z| + 15 s above
