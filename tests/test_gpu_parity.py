@@ -367,6 +367,43 @@ def test_decode_nonfinite_values(kivi, geo_id):
     assert_close(got[fin], ref[fin], f"finite outputs beside the non-finite groups ({geo_id})")
 
 
+def test_v1_batched_and_sparse_decode_extreme_values(kivi):
+    """The multi-query (jac_launch_batched) and sparse-retained entry points on
+    V tokens scaled x3000 (30% of them): the same exact correction as the
+    batch decode keeps every query within max-abs 2e-3 / rel 1e-2 of the
+    float64 two-pass reference."""
+    st = State(V1, lens=[1000], seed=31)
+    rng = np.random.default_rng(31)
+    v = st.v_hist[0].view(np.float16).astype(np.float32)
+    pick = rng.random(v.shape[0]) < 0.3
+    v[pick] *= 3000.0
+    st.v_hist[0] = np.clip(v, -65000, 65000).astype(np.float16).view(np.uint16)
+    st.build_oracle()
+    g = to_torch(st)
+    bt = torch.from_numpy(st.tables[0]).cuda()
+    pool = [g[n] for n in ("k_code", "k_scale", "k_zero", "v_code", "v_scale", "v_zero")]
+    nq = 6
+    qs = rng.standard_normal((nq, 40, 128)).astype(np.float16)
+    seq = np.arange(1000 - nq + 1, 1001).astype(np.int32)
+    out_b = torch.empty((nq, 40, 128), dtype=torch.float32, device="cuda")
+    kivi.kivi_decode_batched_dsl(torch.from_numpy(qs).cuda(), torch.from_numpy(seq).cuda(), bt,
+                                 *pool, g["k_scr"][0], g["v_scr"][0], nq, out_b)
+    torch.cuda.synchronize()
+    for i in range(nq):
+        ref = o.decode_twopass(st.cache, 0, qs[i].view(np.uint16), st.tables[0], int(seq[i]))
+        assert np.abs(ref).max() > 30.0
+        assert_close(out_b[i].cpu().numpy(), ref, f"batched q{i} x3000")
+    compact = np.zeros(124, np.int32)  # the v1 ABI's table width
+    compact[:3] = st.tables[0][[5, 1, 9]]
+    q = torch.from_numpy(st.q[0].copy()).view(torch.float16).cuda()
+    outs = torch.empty((40, 128), dtype=torch.float32, device="cuda")
+    kivi.kivi_decode_sparse_retained_dsl(q, torch.from_numpy(compact).cuda(), *pool,
+                                         g["k_scr"][0], g["v_scr"][0], 1000, 3, outs)
+    torch.cuda.synchronize()
+    ref = o.decode_sparse_retained(st.cache, 0, st.q[0], compact, 1000, 3, twopass=True)
+    assert_close(outs.cpu().numpy(), ref, "sparse retained x3000")
+
+
 def test_caller_workspace_needs_no_initial_contents(kivi):
     """A caller workspace filled with random bytes, then reused by a second
     call with other queries, decodes to the same bits as the library's own
