@@ -289,6 +289,8 @@ _EXTREME_GEOS = {
                                 outliers=4, outlier_scale=10.0, seed=11),
     "hd128_g16_p32": wl.Workload("x128", 32, 2, 128, 1, 4096, 4096, page=32, residual=128,
                                  outliers=4, outlier_scale=10.0, seed=12),
+    "hd64_g7_p16": wl.Workload("x64p", 14, 2, 64, 1, 4096, 4096, page=16, residual=128,
+                               outliers=4, outlier_scale=8.0, seed=13),  # packed QK at HD 64
 }
 
 
@@ -330,7 +332,7 @@ def test_decode_extreme_value_scales(kivi, mults, seed, frac, geo_id):
     assert_close(got, ref, f"values scaled by {mults}")
 
 
-@pytest.mark.parametrize("geo_id", ["hd128_g5", "hd64_g10_p32"])
+@pytest.mark.parametrize("geo_id", ["hd128_g5", "hd64_g10_p32", "hd64_g7_p16"])
 def test_decode_nonfinite_values(kivi, geo_id):
     """+inf in V in a quantised token, -inf in an fp16 residual token.  The
     reference dequantises the first with an infinite scale, 0 * inf = NaN for
