@@ -210,14 +210,31 @@ def test_decode_bytes_formula():
     assert n == 8 * (3968 * 160 + 128 * 512) + 4 * 124 + 40 * 128 * 6
 
 
+def plan_count_closed_form(start, num, residual, group):
+    """Sub-chunks of the greedy plan (source_patch.py:521-546), from the
+    arithmetic alone: the first takes the room left in the scratch,
+    cap - res0; each later one starts from a residual of exactly R (a full
+    scratch of R + 32 rows just aged one group out) and takes one group."""
+    old0 = max(0, start - residual) // group * group
+    room0 = residual + group - (start - old0)
+    return 1 if num <= room0 else 1 + -(-(num - room0) // group)
+
+
 def check_plan(plan, start, num, residual, group):
     cap = residual + group
     seq = start
-    for (s0, n, scratch_start, page, post) in plan:
+    assert len(plan) == plan_count_closed_form(start, num, residual, group)
+    for idx, (s0, n, scratch_start, page, post) in enumerate(plan):
         assert s0 == seq and n >= 1
         old = max(0, s0 - residual) // group * group
         assert scratch_start == s0 - old
         assert scratch_start + n <= cap, "a sub-chunk must fit the scratch"
+        if idx < len(plan) - 1:
+            # greedy: take = min(remaining, room), so every sub-chunk but
+            # the last fills the scratch to its capacity
+            assert scratch_start + n == cap, "a non-final sub-chunk must fill the scratch"
+        else:
+            assert n == start + num - s0
         new_old = max(0, s0 + n - residual) // group * group
         assert new_old - old in (0, group), "at most one age-out per sub-chunk"
         if new_old > old:
@@ -237,6 +254,57 @@ def test_plan_batched_write_invariants_and_oracle(native, oracle, residual, grou
         plan = kivi.plan_batched_write(start, num, residual, group)
         check_plan(plan, start, num, residual, group)
         assert plan == oracle.plan_batched_write(start, num, residual, group)
+
+
+def _mutant_planner(start, num, residual, group, kind):
+    """Plausible mistakes in the planner: an off-by-one room, a take of one
+    group at a time, and room counted from the residual window alone."""
+    cap = residual + group
+    plan, seq, rem = [], start, num
+    while rem > 0:
+        old = max(0, seq - residual) // group * group
+        res = seq - old
+        room = {"room-1": cap - res - 1, "group": group, "residual": residual - res}[kind]
+        take = min(rem, max(room, 1))
+        new_old = max(0, seq + take - residual) // group * group
+        aged = new_old > old
+        plan.append((seq, take, res, old // group if aged else None,
+                     seq + take - new_old if aged else None))
+        seq += take
+        rem -= take
+    return plan
+
+
+@pytest.mark.parametrize("kind", ["room-1", "group", "residual"])
+def test_plan_check_rejects_mutant_planners(kind):
+    """check_plan pins the exact cut: each mutant fails it on some case the
+    real planners pass."""
+    caught = 0
+    for start, num in [(0, 1), (0, 160), (0, 161), (159, 2), (127, 300), (4000, 96), (10, 500)]:
+        try:
+            check_plan(_mutant_planner(start, num, 128, 32, kind), start, num, 128, 32)
+        except AssertionError:
+            caught += 1
+    assert caught > 0
+
+
+def test_plan_closed_form_small_brute_force():
+    """The count formula against a direct simulation of the scratch (append
+    until it holds R + 32 rows, then age one group out) on all small inputs."""
+    for residual, group in ((32, 32), (64, 32), (128, 32)):
+        cap = residual + group
+        for start in range(0, 3 * cap):
+            for num in range(1, 3 * cap):
+                res = start - max(0, start - residual) // group * group
+                chunks, left = 0, num
+                while left:
+                    t = min(left, cap - res)
+                    chunks += 1
+                    left -= t
+                    res += t
+                    if res == cap:
+                        res -= group
+                assert chunks == plan_count_closed_form(start, num, residual, group)
 
 
 def test_plan_batched_write_rejects_like_reference(native):
