@@ -18,17 +18,18 @@
  *     sequence they compute exactly what the v1 symbols compute.
  *
  * Conventions (both groups):
- *  - every pointer is caller-owned device memory.  The library allocates
- *    twice: a pinned status word per device (jacq_kivi_init), and split-K
- *    workspaces for the decodes, one per (device, stream): the v1 decode
- *    symbols always use them, the jacq_kivi_* decodes when the caller passes
- *    none.  A stream's workspace is allocated on its first decode for at
- *    least 256 sequences and replaced by a larger one when a larger batch
- *    needs it; the smaller one is kept until the process ends, since a
- *    captured graph may still use it.  So a graph capture of a decode
- *    allocates nothing once a call of at least its batch (or of at most 256
- *    sequences) has run on its stream outside the capture.  The writers never
- *    allocate;
+ *  - every pointer is caller-owned device memory.  The v1 symbols and the
+ *    writers never allocate: the v1 decodes take their split-K workspace from
+ *    static device arrays of the library (8 regions of 16 MiB per GPU, one
+ *    per stream that runs v1 decodes, held until the process ends; a ninth
+ *    stream's v1 decode is an error).  The library allocates a pinned status
+ *    word per device (jacq_kivi_init) and, for jacq_kivi_decode /
+ *    jacq_kivi_decode_sparse_retained calls that pass no workspace, one
+ *    split-K workspace per (device, stream), at most 16 streams per device:
+ *    allocated on the stream's first such decode for at least 256 sequences
+ *    and replaced by a larger one when a larger batch needs it; the smaller
+ *    one is kept (a captured graph may still use it) until
+ *    jacq_kivi_release_workspaces;
  *  - every call is asynchronous on `stream`; a cache write followed by a
  *    decode on the same stream is ordered;
  *  - fp16 tensors are IEEE binary16 bit patterns (jacq_half_t), bit
@@ -227,14 +228,31 @@ int jacq_kivi_init(void);
  * (when not NULL; flags a timed-out merge left behind would otherwise be read
  * by a graph replay carrying the same epoch), clears the word and returns
  * JACQ_KIVI_ETIMEOUT; otherwise JACQ_KIVI_OK.  Call it with no decode running
- * on the device. */
+ * on the device.  A timed-out merge also poisons the workspace it ran on
+ * (its first 8 bytes): until that workspace is zeroed here, every merged
+ * segment of a decode on it -- a graph replay included, which never passes
+ * through the host checks -- is NaN and sets the status word again, never a
+ * finite value built from a stale partial. */
 int jacq_kivi_decode_status(void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Frees every split-K workspace the library allocated on the current device
+ * for jacq_kivi_* decodes without a workspace (no counterpart in the
+ * reference).  It synchronises the device first.  Graphs captured with such a
+ * decode hold the freed addresses and must not be replayed afterwards.  The
+ * static arrays (v1 decodes, jacq_kivi_decode_noalloc) are not affected. */
+int jacq_kivi_release_workspaces(void);
 
 /* Test hook (no counterpart in the reference): with microseconds > 0 every
  * later matrix-core decode's merge waits for a tag that no wavefront stores
  * and gives up after that long, so tests can force the time-out path from the
  * host (every kernel still exits normally).  0 restores normal operation. */
 void jacq_kivi_test_force_merge_timeout(uint32_t microseconds);
+
+/* Test hook (no counterpart in the reference): device allocations
+ * (hipMalloc) the library has made in this process -- the split-K
+ * workspaces of jacq_kivi_* decodes called without one.  The v1 symbols, the
+ * writers and jacq_kivi_decode_noalloc never add to it. */
+int64_t jacq_kivi_test_device_allocations(void);
 
 /* Geometry check (integrations/vllm_kivi/layout.py:51-74 and the supported
  * geometry checks of source_patch.py:744-756, generalised). */

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <cstdio>
 #include <cstdlib>
@@ -99,6 +100,19 @@ struct StreamWorkspace {
 constexpr size_t kNoAllocScratchBytes = 32u << 20;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
+// Split-K workspaces of the v1 decode symbols (jac_launch*), which allocate
+// nothing either (the reference's launch contract: every buffer is the
+// caller's, source_patch.py:2391-2417).  A static device array of
+// kV1Regions regions; a stream takes the next free region on its first v1
+// decode and keeps it (decodes on different streams may run at once, and a
+// graph captured on a stream keeps its region's address).  A call whose
+// queries need more than one region holds is split into launches of as many
+// queries as fit, one after another on the stream (each query's result does
+// not depend on which launch decodes it).
+constexpr int kV1Regions = 8;
+constexpr size_t kV1RegionBytes = 16u << 20;
+static __device__ __align__(256) uint8_t v1_workspace[kV1Regions * kV1RegionBytes];
+
 struct DeviceState {
   int cus = 0;
   void* scratch_ptr = nullptr;  // this device's copy of `scratch`
@@ -107,11 +121,15 @@ struct DeviceState {
   // synchronisation, cleared by jacq_kivi_decode_status.
   volatile uint32_t* status = nullptr;
   uint32_t* status_dev = nullptr;  // the same word, as the device addresses it
+  void* v1_ptr = nullptr;  // this device's copy of `v1_workspace`
+  std::vector<hipStream_t> v1_streams;  // stream holding region i
   std::vector<StreamWorkspace> ws;
   std::vector<StreamWorkspace> retired;
 };
 std::mutex g_mu;
 std::vector<DeviceState> g_dev;
+// device allocations the library has made (jacq_kivi_test_device_allocations)
+std::atomic<int64_t> g_device_allocations{0};
 
 // Per-device set-up, once, with the device current.  Called by every entry
 // point (and by jacq_kivi_init); everything it allocates lives until exit.
@@ -142,6 +160,29 @@ int init_device_locked(int dev) {
       return fail(JACQ_KIVI_EHIP, "hipGetSymbolAddress(scratch) failed");
     s.scratch_ptr = ptr;
   }
+  if (!s.v1_ptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(v1_workspace)) != hipSuccess || !ptr)
+      return fail(JACQ_KIVI_EHIP, "hipGetSymbolAddress(v1_workspace) failed");
+    s.v1_ptr = ptr;
+  }
+  return JACQ_KIVI_OK;
+}
+
+// The v1 workspace region of `stream` on device `dev` (set up).
+int v1_region(int dev, hipStream_t stream, void** out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceState& s = g_dev[dev];
+  size_t i = 0;
+  while (i < s.v1_streams.size() && s.v1_streams[i] != stream) ++i;
+  if (i == s.v1_streams.size()) {
+    if (i == (size_t)kV1Regions)
+      return fail(JACQ_KIVI_ENOMEM, "v1 decodes on more than " + std::to_string(kV1Regions) +
+                                         " streams of one device (each stream keeps one of the "
+                                         "library's static split-K workspace regions)");
+    s.v1_streams.push_back(stream);
+  }
+  *out = (uint8_t*)s.v1_ptr + i * kV1RegionBytes;
   return JACQ_KIVI_OK;
 }
 
@@ -185,6 +226,8 @@ constexpr const char* kTimeoutMsg =
 // Sequences the library's own split-K workspace covers from its first use
 // (about 13 MB at the v1 geometry).
 constexpr int kLibraryWorkspaceBatch = 256;
+// Streams per device that may hold a library workspace at once.
+constexpr int kLibraryWorkspaceStreams = 16;
 
 int library_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
   std::lock_guard<std::mutex> lk(g_mu);
@@ -193,6 +236,11 @@ int library_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
   for (auto& x : s.ws)
     if (x.stream == stream) w = &x;
   if (!w) {
+    if (s.ws.size() >= (size_t)kLibraryWorkspaceStreams)
+      return fail(JACQ_KIVI_ENOMEM,
+                  "library split-K workspaces exist for " + std::to_string(s.ws.size()) +
+                      " streams of this device, the maximum; pass a workspace or call "
+                      "jacq_kivi_release_workspaces()");
     s.ws.push_back({stream, nullptr, 0});
     w = &s.ws.back();
   }
@@ -206,6 +254,7 @@ int library_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
     // captured on a fresh stream); an allocation is not a stream operation,
     // so this thread's capture mode is relaxed around it, as the runtime
     // allows, instead of invalidating the capture.
+    g_device_allocations.fetch_add(1, std::memory_order_relaxed);
     hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
     const bool swapped = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
     const hipError_t me = hipMalloc(&p, want);
@@ -228,9 +277,23 @@ int library_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
 // can see bounds every sequence's count.
 struct SplitPlan {
   int max_splits;
+  int runs_cap;  // per-query split: runs of the longest sequence (0: whole-call split)
 };
 
-SplitPlan plan_splits(int64_t max_tokens) { return {jacq::split_count(max_tokens)}; }
+SplitPlan plan_splits(int64_t max_tokens) { return {jacq::split_count(max_tokens), 0}; }
+
+// Per-query split plan: a query of up to max_tokens tokens is cut into at
+// most this many runs (the kernel's stream_waves of its units).
+// A query of at most max_tokens tokens has T <= ceil(max_tokens / 32) tiles,
+// at most R / 32 + 1 of them fp16 residual tiles, so its units (quantised
+// groups + 3 per residual tile = T + 2 residual tiles) are bounded by
+// T + 2 (R / 32 + 1) per kv head, whatever its length.
+SplitPlan plan_splits_per_query(const KiviGeo& g, int64_t max_tokens, int waves) {
+  const int64_t tiles = std::max<int64_t>(1, (max_tokens + jacq::kGroup - 1) / jacq::kGroup);
+  const int64_t units = (int64_t)g.nkv * (tiles + 2 * (g.residual / jacq::kGroup + 1));
+  const int64_t runs = std::min<int64_t>(waves, std::max<int64_t>(1, (units + 3) / 4));
+  return {jacq::split_count(max_tokens), (int)runs};
+}
 
 // JACQ_KIVI_DECODE=simple selects the VALU decode kernel (a cross-check of
 // the matrix-core kernel); the default is the matrix-core kernel.
@@ -245,9 +308,12 @@ bool use_simple_decode() {
 // Partial-result slots: VALU kernel -- one per (sequence, kv head, split);
 // matrix-core kernel -- one per (sequence, kv head) plus one per wavefront
 // (a wavefront's run cuts at most one extra piece off the stream).
+// Per-query split (the v1 symbols): one per (query, kv head) plus one per
+// run of each query, at most runs_cap (the runs of the longest sequence).
 size_t partial_slots(const KiviGeo& g, int batch, const SplitPlan& sp, int waves) {
   if (use_simple_decode())
     return sp.max_splits <= 1 ? 0 : (size_t)batch * g.nkv * sp.max_splits;
+  if (sp.runs_cap > 0) return (size_t)batch * ((size_t)g.nkv + (size_t)sp.runs_cap);
   return (size_t)batch * g.nkv + (size_t)waves;
 }
 
@@ -255,10 +321,16 @@ size_t partial_slots(const KiviGeo& g, int batch, const SplitPlan& sp, int waves
 // and, for the matrix-core kernel, [epoch uint64 per slot] (8-byte aligned:
 // G * (HD + 2) floats per slot is even).  The flags need no initial contents:
 // a flag counts only when it holds the current launch's 64-bit epoch.
+// A 16-byte header comes first: the poison word the matrix-core kernel's
+// merge sets when a wait runs out (it must sit at the same place whatever the
+// batch of the calls sharing the workspace).
+constexpr size_t kWorkspaceHeader = 16;
+
 size_t workspace_bytes(const KiviGeo& g, int batch, const SplitPlan& sp, int waves) {
   const size_t slots = partial_slots(g, batch, sp, waves);
+  if (slots == 0) return 0;
   const size_t flags = use_simple_decode() ? 0 : slots * sizeof(uint64_t);
-  return slots * g.gqa * (size_t)(g.hd + 2) * sizeof(float) + flags;
+  return kWorkspaceHeader + slots * g.gqa * (size_t)(g.hd + 2) * sizeof(float) + flags;
 }
 
 void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& sp, int waves,
@@ -266,8 +338,10 @@ void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& 
   a.max_splits = sp.max_splits;
   a.batch = batch;
   a.waves = waves;
+  a.per_query = sp.runs_cap > 0;
   const size_t slots = partial_slots(g, batch, sp, waves) * g.gqa;
-  a.ws_ml = (float*)ws;
+  a.ws_poison = (uint64_t*)ws;
+  a.ws_ml = ws ? (float*)((uint8_t*)ws + kWorkspaceHeader) : nullptr;
   a.ws_acc = ws ? a.ws_ml + slots * 2 : nullptr;
   a.ws_flag = ws ? (uint64_t*)(a.ws_acc + slots * g.hd) : nullptr;
 }
@@ -322,7 +396,8 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
                const jacq_half_t* ksc, const jacq_half_t* kz, const uint8_t* vc,
                const jacq_half_t* vsc, const jacq_half_t* vz, const jacq_half_t* kscr,
                const jacq_half_t* vscr, int64_t scr_stride, int batch, float* O, void* ws,
-               size_t ws_bytes, hipStream_t stream, int retained_pages = -1) {
+               size_t ws_bytes, hipStream_t stream, int retained_pages = -1,
+               bool per_query = false) {
   if (!aligned16({Q, O, kc, ksc, kz, vc, vsc, vz, kscr, vscr, ws}))
     return fail(JACQ_KIVI_EINVAL, "tensor and workspace pointers must be 16-byte aligned");
   const KiviGeo g = make_geo(x);
@@ -336,8 +411,9 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
     jacq::window_of(g, retained_pages, seq_len_host, &ov, &rv);
     max_tokens = ov + rv;
   }
-  const SplitPlan sp = plan_splits(max_tokens);
   const int waves = jacq::decode_stream_waves(g, ds.cus);
+  const SplitPlan sp =
+      per_query ? plan_splits_per_query(g, max_tokens, waves) : plan_splits(max_tokens);
   const size_t need = workspace_bytes(g, batch, sp, waves);
   if (need > 0) {
     if (ws == nullptr) {
@@ -428,6 +504,39 @@ int run_append(const jacq_kivi_geometry& x, uint8_t* kc, jacq_half_t* ksc, jacq_
   return JACQ_KIVI_OK;
 }
 
+// Decode of the v1 symbols: the per-query split (every query decodes to the
+// same bits whatever else the call holds) and the stream's static workspace
+// region, so nothing is allocated.  Queries beyond what one region holds go
+// to further launches on the stream.
+int v1_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t* seq_lens,
+              int seq_len_host, const int32_t* bt, const uint8_t* kc, const jacq_half_t* ksc,
+              const jacq_half_t* kz, const uint8_t* vc, const jacq_half_t* vsc,
+              const jacq_half_t* vz, const jacq_half_t* kscr, const jacq_half_t* vscr,
+              int queries, float* O, hipStream_t stream, int retained_pages = -1) {
+  int dev = 0;
+  if (int e = current_device(&dev)) return e;
+  void* region = nullptr;
+  if (int e = v1_region(dev, stream, &region)) return e;
+  const KiviGeo g = make_geo(x);
+  const int waves = jacq::decode_stream_waves(g, device_state(dev).cus);
+  const SplitPlan sp = plan_splits_per_query(g, max_seq_len(x), waves);
+  const size_t one = workspace_bytes(g, 1, sp, waves);
+  const size_t per = one > kWorkspaceHeader ? one - kWorkspaceHeader : 0;
+  const int chunk =
+      per == 0 ? queries
+               : (int)std::min<size_t>((size_t)queries, (kV1RegionBytes - kWorkspaceHeader) / per);
+  if (chunk < 1) return fail(JACQ_KIVI_ENOMEM, "one query needs more than a v1 workspace region");
+  const int64_t qs = (int64_t)g.nh * g.hd;
+  for (int q0 = 0; q0 < queries; q0 += chunk) {
+    const int n = std::min(chunk, queries - q0);
+    if (int e = run_decode(x, Q + q0 * qs, seq_lens ? seq_lens + q0 : nullptr, seq_len_host, bt, 0,
+                           kc, ksc, kz, vc, vsc, vz, kscr, vscr, 0, n, O + q0 * qs, region,
+                           kV1RegionBytes, stream, retained_pages, true))
+      return e;
+  }
+  return JACQ_KIVI_OK;
+}
+
 // CUDA_CHECK of the emitted v1 symbols: report and exit(1).  A merge
 // time-out of an earlier decode is reported the same way by the next v1
 // decode on the device.
@@ -475,6 +584,7 @@ int jacq_kivi_decode_status(void* workspace, size_t workspace_bytes_, hipStream_
     all = g_dev[dev].ws;
     all.insert(all.end(), g_dev[dev].retired.begin(), g_dev[dev].retired.end());
     all.push_back({stream, g_dev[dev].scratch_ptr, kNoAllocScratchBytes});
+    all.push_back({stream, g_dev[dev].v1_ptr, kV1Regions * kV1RegionBytes});
   }
   if (workspace && workspace_bytes_) all.push_back({stream, workspace, workspace_bytes_});
   for (const auto& w : all)
@@ -483,6 +593,26 @@ int jacq_kivi_decode_status(void* workspace, size_t workspace_bytes_, hipStream_
   *ds.status = 0;
   return fail(JACQ_KIVI_ETIMEOUT, "a split-K merge timed out since the last query; its "
                                   "outputs were NaN; the workspaces are reset");
+}
+
+int jacq_kivi_release_workspaces(void) {
+  int dev = 0;
+  if (int e = current_device(&dev)) return e;
+  if (hipDeviceSynchronize() != hipSuccess) return fail(JACQ_KIVI_EHIP, "hipDeviceSynchronize failed");
+  std::vector<StreamWorkspace> all;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    all.swap(g_dev[dev].ws);
+    all.insert(all.end(), g_dev[dev].retired.begin(), g_dev[dev].retired.end());
+    g_dev[dev].retired.clear();
+  }
+  for (const auto& w : all)
+    if (w.ptr && hipFree(w.ptr) != hipSuccess) return fail(JACQ_KIVI_EHIP, "hipFree failed");
+  return JACQ_KIVI_OK;
+}
+
+int64_t jacq_kivi_test_device_allocations(void) {
+  return g_device_allocations.load(std::memory_order_relaxed);
 }
 
 void jacq_kivi_test_force_merge_timeout(uint32_t microseconds) {
@@ -635,7 +765,6 @@ int jacq_kivi_cache_append(const jacq_kivi_geometry* geo, uint8_t* K_CODE_PAGES,
                     BLOCK_TABLES, geo->max_pages_per_seq, START_LENS, 0, num_new, batch, stream);
 }
 
-// plan_batched_write, source_patch.py:504-553.
 int jacq_kivi_profile_start(int32_t max_calls, int32_t split) {
   if (max_calls < 1) return fail(JACQ_KIVI_EINVAL, "max_calls must be >= 1");
   std::lock_guard<std::mutex> lk(g_prof_mu);
@@ -689,6 +818,7 @@ int32_t jacq_kivi_profile_write_ms(float* ms, int32_t cap) {
   return n;
 }
 
+// plan_batched_write, source_patch.py:504-553.
 int32_t jacq_kivi_plan_batched_write(int32_t start_seq_len, int32_t num_new, int32_t residual,
                                      int32_t group, jacq_kivi_subchunk* out, int32_t cap) {
   if (start_seq_len < 0)
@@ -733,9 +863,9 @@ void jac_launch(const jacq_half_t* Q, const int32_t* BLOCK_TABLE, const uint8_t*
                 const jacq_half_t* V_ZERO_PAGES, const jacq_half_t* K_RESIDUAL_SCRATCH,
                 const jacq_half_t* V_RESIDUAL_SCRATCH, int SEQ_LEN, float* O,
                 hipStream_t stream) {
-  v1_check(run_decode(kGlobal, Q, nullptr, SEQ_LEN, BLOCK_TABLE, 0, K_CODE_PAGES, K_SCALE_PAGES,
-                      K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES,
-                      K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, 0, 1, O, nullptr, 0, stream),
+  v1_check(v1_decode(kGlobal, Q, nullptr, SEQ_LEN, BLOCK_TABLE, K_CODE_PAGES, K_SCALE_PAGES,
+                     K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES, K_RESIDUAL_SCRATCH,
+                     V_RESIDUAL_SCRATCH, 1, O, stream),
            "jac_launch");
 }
 
@@ -746,9 +876,9 @@ void jac_launch_tp2_local(const jacq_half_t* Q, const int32_t* BLOCK_TABLE,
                           const jacq_half_t* K_RESIDUAL_SCRATCH,
                           const jacq_half_t* V_RESIDUAL_SCRATCH, int SEQ_LEN, float* O,
                           hipStream_t stream) {
-  v1_check(run_decode(kTp2Local, Q, nullptr, SEQ_LEN, BLOCK_TABLE, 0, K_CODE_PAGES,
-                      K_SCALE_PAGES, K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES,
-                      K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, 0, 1, O, nullptr, 0, stream),
+  v1_check(v1_decode(kTp2Local, Q, nullptr, SEQ_LEN, BLOCK_TABLE, K_CODE_PAGES, K_SCALE_PAGES,
+                     K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES, K_RESIDUAL_SCRATCH,
+                     V_RESIDUAL_SCRATCH, 1, O, stream),
            "jac_launch_tp2_local");
 }
 
@@ -759,9 +889,8 @@ static void sparse_v1(const jacq_kivi_geometry& x, const jacq_half_t* Q,
                       const jacq_half_t* vscr, int SEQ_LEN, int NUM_RETAINED_PAGES, float* O,
                       hipStream_t stream, const char* where) {
   // the kernel clamps NUM_RETAINED_PAGES to [0, dense old pages] itself
-  v1_check(run_decode(x, Q, nullptr, SEQ_LEN, RETAINED_BLOCK_TABLE, 0, kc, ks, kz, vc, vs, vz,
-                      kscr, vscr, 0, 1, O, nullptr, 0, stream,
-                      NUM_RETAINED_PAGES < 0 ? 0 : NUM_RETAINED_PAGES),
+  v1_check(v1_decode(x, Q, nullptr, SEQ_LEN, RETAINED_BLOCK_TABLE, kc, ks, kz, vc, vs, vz, kscr,
+                     vscr, 1, O, stream, NUM_RETAINED_PAGES < 0 ? 0 : NUM_RETAINED_PAGES),
            where);
 }
 
@@ -795,8 +924,8 @@ static void batched_v1(const jacq_kivi_geometry& x, const jacq_half_t* Q, const 
                        const jacq_half_t* vz, const jacq_half_t* kscr, const jacq_half_t* vscr,
                        int NUM_QUERIES, float* O, hipStream_t stream, const char* where) {
   if (NUM_QUERIES < 1) return;  // an empty grid: the reference launch would be a no-op error
-  v1_check(run_decode(x, Q, SEQ_LENS, -1, BLOCK_TABLE, 0, kc, ks, kz, vc, vs, vz, kscr, vscr, 0,
-                      NUM_QUERIES, O, nullptr, 0, stream),
+  v1_check(v1_decode(x, Q, SEQ_LENS, -1, BLOCK_TABLE, kc, ks, kz, vc, vs, vz, kscr, vscr,
+                     NUM_QUERIES, O, stream),
            where);
 }
 

@@ -253,19 +253,22 @@ __device__ inline uint32_t lds_addr(const void* p) {
 // it past the caches sustains a markedly higher HBM read rate.
 // The instruction's immediate offset moves the LDS address as well as the
 // global one, so M0 gets dst - OFF.  M0 is set inside the same asm statement,
-// so nothing the compiler keeps in M0 is live across it.
+// so nothing the compiler keeps in M0 is live across it.  An LDS DMA must not
+// read M0 in the instruction right after the SALU write of it (the GFX9
+// M0 / LDS-DMA hazard: one wait state); the compiler's hazard recognizer does
+// not look inside asm, so the s_nop is written here.
 template <int SZ, int OFF>
 __device__ inline void dma(uint64_t addr, uint32_t dst) {
   static_assert(OFF >= 0 && OFF < 4096, "global immediate offset range");
   const uint32_t m0 = dst - OFF;
   if constexpr (SZ == 16)
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off offset:%2 nt"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off offset:%2 nt"
                  :: "s"(m0), "v"(addr), "n"(OFF) : "memory", "m0");
   else if constexpr (SZ == 4)
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off offset:%2 nt"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off offset:%2 nt"
                  :: "s"(m0), "v"(addr), "n"(OFF) : "memory", "m0");
   else
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_ushort %1, off offset:%2 nt"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_ushort %1, off offset:%2 nt"
                  :: "s"(m0), "v"(addr), "n"(OFF) : "memory", "m0");
 }
 
@@ -274,7 +277,7 @@ template <int OFF>
 __device__ inline void dma16s(uint64_t sbase, uint32_t voff, uint32_t dst) {
   static_assert(OFF >= 0 && OFF < 4096, "global immediate offset range");
   const uint32_t m0 = dst - OFF;
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2 offset:%3 nt"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:%3 nt"
                :: "s"(m0), "v"(voff), "s"(sbase), "n"(OFF) : "memory", "m0");
 }
 
@@ -875,6 +878,59 @@ __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, in
   return rt;
 }
 
+// ---- per-query split (the v1 symbols) ----
+//
+// Each query's streams (NKV x its units) are cut into stream_waves(its units)
+// equal runs by its own length alone, exactly as a call with that query alone
+// cuts them, whatever the other queries of the call are: every query decodes
+// to the same bits in a batched call as in a single one (variants.rs:1211-1213
+// expects the batched kernel to match the single-token one bit for bit).  The
+// runs of all queries are numbered query by query; the stream wavefronts take
+// them in turn.
+struct RunLoc {
+  int q;       // query, or -1 past the last run
+  int units;   // units per kv head of the query
+  int runs;    // runs of the query
+  int64_t r0;  // global index of the query's first run
+};
+
+__device__ inline int query_runs(const KiviGeo& g, const DecodeArgs& a, int units) {
+  return (int)stream_waves((int64_t)g.nkv * units, a.waves);
+}
+
+__device__ inline RunLoc locate_run(const KiviGeo& g, const DecodeArgs& a, int64_t r, int lane) {
+  int64_t acc = 0;
+  for (int base = 0; base < a.batch; base += 64) {
+    const int bb = base + lane;
+    int U = 0, R = 0;
+    if (bb < a.batch) {
+      U = seq_units(g, a, bb);
+      R = query_runs(g, a, U);
+    }
+    const int incl = wave_incl_scan(R, lane);
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(bb < a.batch && acc + incl > r);
+    if (hit) {
+      const int f = __builtin_ctzll(hit);
+      const int Rf = __builtin_amdgcn_readlane(R, f);
+      return {base + f, __builtin_amdgcn_readlane(U, f), Rf,
+              acc + __builtin_amdgcn_readlane(incl, f) - Rf};
+    }
+    acc += __builtin_amdgcn_readlane(incl, 63);
+  }
+  return {-1, 0, 0, acc};
+}
+
+// Global index of query b's first run.
+__device__ inline int64_t query_run_start(const KiviGeo& g, const DecodeArgs& a, int b, int lane) {
+  int64_t run = 0;
+  for (int base = 0; base < b; base += 64) {
+    const int bb = base + lane;
+    const int R = bb < b ? query_runs(g, a, seq_units(g, a, bb)) : 0;
+    run += __builtin_amdgcn_readfirstlane(wave_sum_i(R));
+  }
+  return run;
+}
+
 // ---- split-K merge, run by workgroups of the same launch ----
 //
 // The stream wavefronts fill every slot of the device, so the merge
@@ -893,6 +949,10 @@ __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, in
 // merge wavefront that still waits after kMergeTimeoutTicks (s_memrealtime,
 // 100 MHz) writes NaN for its segments and ends, so the launch always drains.
 constexpr uint64_t kMergeTimeoutTicks = 100000000;  // 1 s
+// Value of a workspace's poison word (its first 8 bytes) after a merge on it
+// timed out; anything else means clean (a fresh buffer matches with
+// probability 2^-64).
+constexpr uint64_t kWorkspacePoison = 0x4A4B49564954494Dull;
 
 // Test-only (jacq_kivi_test_force_merge_timeout): when nonzero, every merge
 // waits for an epoch no stream wave stores and gives up after this many
@@ -932,9 +992,13 @@ __device__ inline void st_agent(void* p, float lo, float hi) {
 }
 // 16-byte agent-scope store (the bits the compiler gives an agent-scope
 // relaxed atomic store, sc1, on a four-dword store); waited for by the
-// explicit vmcnt(0) before the partial's flag
+// explicit vmcnt(0) before the partial's flag.  A VALU write of the data
+// VGPRs of a store wider than 8 bytes needs one wait state after it (a GFX9
+// hazard the compiler's recognizer cannot see inside asm): without the s_nop
+// the next instruction may overwrite data the store has not read yet, and a
+// lane's 16 bytes of a partial were now and then stored wrong.
 __device__ inline void st_agent4(float* p, floatx4 v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(p), "v"(v) : "memory");
 }
 // 16-byte agent-scope load; the caller waits with an explicit vmcnt(0) and
 // then passes the value through keep() so no use moves above the wait
@@ -974,16 +1038,22 @@ __device__ inline void write_stamp(const DecodeArgs& a, uint64_t t0, uint64_t in
 // likewise, O = acc / max(L, 1e-30), in the log2 domain of the decode loop.
 // The pieces of a segment are recomputed from the same split the stream
 // wavefronts used; a segment with a single non-empty piece was written whole.
-template <int HD, bool PACK>
+template <int HD, bool PACK, bool PQ>
 __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) {
   constexpr int K = (PACK ? 8 : 16) * HD / 256;  // float4 outputs per lane: G * HD <= 256 K
   constexpr int U = K <= 2 ? 8 : K > 4 ? 1 : 2;  // partials whose loads are in flight together
   const int G = g.gqa, NKV = g.nkv, n4 = G * HD / 4;
-  const int64_t TT = stream_units(g, a, lane);
-  const int64_t W = stream_waves(TT, a.waves);
+  // the whole call's stream (per-query split: each segment's own query, below)
+  const int64_t TT = PQ ? 0 : stream_units(g, a, lane);
+  const int64_t W = PQ ? 0 : stream_waves(TT, a.waves);
   const int nseg = a.batch * NKV;
   const uint64_t epoch = a.epoch + a.merge_skew, t_start = __builtin_amdgcn_s_memrealtime();
-  bool late = false;  // wave-uniform: the wait ran out
+  // wave-uniform: the wait ran out.  A merge of an earlier launch on this
+  // workspace that timed out left the poison word set: flags its stream
+  // wavefronts stored after it gave up may carry the epoch a replayed graph
+  // repeats, so until the host resets the workspace every merged segment is
+  // NaN and no flag is consumed.
+  bool late = a.ws_poison && ld_agent(a.ws_poison) == kWorkspacePoison;
   int gi[K], d[K];
   bool on[K];
 #pragma unroll
@@ -999,11 +1069,22 @@ __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) 
     const int T = seq_tiles(g, a, b, &ov, &n);
     const int nq = ov / kGroup;
     const int units = nq + kResidualUnits * (T - nq);
-    const int64_t S0 = seq_start(g, a, b, lane) + (int64_t)h * units, S1 = S0 + units;
-    const int64_t w0 = wave_of(S0, TT, W), w1 = wave_of(S1 - 1, TT, W);
+    // the stream the segment's runs cut (sq units in wq runs), the segment's
+    // first unit in it, and the global index of that stream's first run
+    int64_t sq = TT, wq = W, S0, roff = 0;
+    if constexpr (PQ) {
+      sq = (int64_t)NKV * units;
+      wq = stream_waves(sq, a.waves);
+      S0 = (int64_t)h * units;
+      roff = query_run_start(g, a, b, lane);
+    } else {
+      S0 = seq_start(g, a, b, lane) + (int64_t)h * units;
+    }
+    const int64_t S1 = S0 + units;
+    const int64_t w0 = wave_of(S0, sq, wq), w1 = wave_of(S1 - 1, sq, wq);
     // non-empty pieces: the runs that own at least one tile of the segment
     auto owns = [&](int64_t w) {
-      const int64_t x0 = max(run_begin(w, TT, W), S0), x1 = min(run_begin(w + 1, TT, W), S1);
+      const int64_t x0 = max(run_begin(w, sq, wq), S0), x1 = min(run_begin(w + 1, sq, wq), S1);
       return tile_at((int)(x0 - S0), nq) < tile_at((int)(x1 - S0), nq);
     };
     int pieces = 0;
@@ -1023,7 +1104,7 @@ __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) 
     for (int64_t wb = w0; wb <= w1 && !late; wb += 64) {
       const int64_t wl = wb + lane;
       const bool mine = wl <= w1 && owns(wl);
-      const uint64_t* flag = a.ws_flag + seg + wl;
+      const uint64_t* flag = a.ws_flag + seg + roff + wl;
       uint64_t todo = __builtin_amdgcn_ballot_w64(mine);
       // fold the partials in piece order (the result does not depend on
       // timing), each run of them as soon as its flags show this launch's
@@ -1054,7 +1135,7 @@ __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) 
           for (int u = 0; u < U; ++u) {
             slot[u] = -1;
             if (ready) {
-              slot[u] = seg + wb + __builtin_ctzll(ready);
+              slot[u] = seg + roff + wb + __builtin_ctzll(ready);
               ready &= ready - 1;
             }
           }
@@ -1083,7 +1164,7 @@ __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) 
           // read: clear the flags, so the next launch starts from zero even
           // when it carries the same epoch (a replayed graph does)
           if (consumed & bit)
-            __hip_atomic_store(a.ws_flag + seg + wl, 0ull, __ATOMIC_RELAXED,
+            __hip_atomic_store(a.ws_flag + seg + roff + wl, 0ull, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
           for (int u = 0; u < U; ++u) {
@@ -1109,64 +1190,33 @@ __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) 
         *(floatx4*)(out + (int64_t)gi[k] * HD + d[k]) =
             late ? floatx4{NAN, NAN, NAN, NAN} : acc[k] / fmaxf(Lsum[k], 1.0e-30f);
   }
-  // a wait ran out: the host sees it in the device's status word
-  if (late && lane == 0 && a.status)
-    __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  // a wait ran out (or an earlier one poisoned the workspace): the workspace
+  // stays poisoned, and the host sees it in the device's status word
+  if (late && lane == 0) {
+    if (a.ws_poison)
+      __hip_atomic_store(a.ws_poison, kWorkspacePoison, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (a.status) __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
 }
 
+// One run of the stream: units [x0, x1) of the concatenated (sequence, kv
+// head) streams, starting in sequence sp.b.  `first_seg` with first_* gives
+// the first segment's window when the caller has it already.  Partials of cut
+// segments go to slot b * NKV + h + w (w: the run's index), their flags after
+// the run.  Returns the s_memrealtime of the first group in LDS (profiling).
 template <int HD, int P, bool PACK>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
-    min_waves_per_simd<HD, PACK>()))) void kivi_decode_stream_kernel(KiviGeo g, DecodeArgs a) {
+__device__ __attribute__((always_inline)) inline uint64_t stream_run(
+    const KiviGeo& g, const DecodeArgs& a, StageBuf<HD>* ring, uint16_t* qrows, const Nibble& nb,
+    float sscale, int lane, int64_t x0, int64_t x1, SeqSpan sp, bool first_seg, int first_T,
+    int first_ov, int first_n, int w) {
   using C = Cfg<HD, P>;
   constexpr int KS = C::KS, CPL = C::CPL;
   constexpr int L = stage_loads<HD>(), S = stages<HD, PACK>();
-  static_assert(S >= 2 && S <= 4, "wait_stages covers up to 3 stages in flight");
-  __shared__ __attribute__((aligned(16))) StageBuf<HD> ring[S];
-  // Q rows of the current segment, one per MFMA column head (rows past G stay zero)
-  // Q rows padded by 16 bytes: at a 2 HD-byte stride (a multiple of the 256
-  // bytes the LDS banks span) the rows' k-step reads would all hit the same
-  // banks, an 8-way conflict on every read
   constexpr int QROW = HD + 8;
-  __shared__ __attribute__((aligned(16))) uint16_t qrows[(PACK ? 8 : 16) * QROW];
-
-  const int lane = threadIdx.x, c = lane & 15, j = lane >> 4;
-  const uint64_t t_start = a.stamps ? __builtin_amdgcn_s_memrealtime() : 0;
-  if ((int)blockIdx.x >= a.waves) {
-    merge_segments<HD, PACK>(g, a, lane);
-    write_stamp(a, t_start, 0, lane);
-    return;
-  }
+  const int c = lane & 15, j = lane >> 4;
   const int G = g.gqa, NKV = g.nkv;
-  // Up to 64 sequences, one length load per lane serves the stream's total,
-  // the run's first sequence and that sequence's window: the first block-table
-  // read waits for one memory round, not three.
-  const bool one_pass = a.batch <= 64;
-  int lane_T = 0, lane_ov = 0, lane_n = 0, lane_U = 0;
-  if (one_pass && lane < a.batch) {
-    lane_T = seq_tiles(g, a, lane, &lane_ov, &lane_n);
-    lane_U = lane_ov / kGroup + kResidualUnits * (lane_T - lane_ov / kGroup);
-  }
-  const int lane_incl = wave_incl_scan(lane_U, lane);
-  const int64_t TT = one_pass ? (int64_t)NKV * __builtin_amdgcn_readlane(lane_incl, 63)
-                              : stream_units(g, a, lane);
-  const int64_t W = stream_waves(TT, a.waves);
-  const int w = blockIdx.x;
-  if (w >= W) return;
-  const int64_t x0 = (int64_t)w * TT / W, x1 = (int64_t)(w + 1) * TT / W;
-  if (x0 >= x1) return;
-
-  const Nibble nb;
   const bool sum_col = sum_lane<HD>(c);
   constexpr int C1 = kGroup / CPL - 1;  // a sum column (the first group's)
-  // the ones block of every stage (the DMAs never write it)
-  if (lane < 32) {
-#pragma unroll
-    for (int s_ = 0; s_ < S; ++s_) ((uint32_t*)ring[s_].ones)[lane] = 0x3C003C00u;
-  }
-  // rows past G are read as zeros by the columns that carry no head
-  for (int i = lane; i < (int)(sizeof(qrows) / 16); i += 64) ((u32x4*)qrows)[i] = u32x4{0u, 0u, 0u, 0u};
-  const float sscale = 1.4426950408889634f / __builtin_sqrtf((float)HD);  // log2(e)/sqrt(HD)
-
   // Issue arbitration favours the oldest of the waves sharing a SIMD, which left
   // alone finishes its run well before the younger ones.  Each wave drops its
   // priority at 1/2, 4/5 and 19/20 of its own run, so a wave behind its
@@ -1190,21 +1240,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
       level = 0;
     }
   };
-  SeqSpan sp;
-  int first_T = 0, first_ov = 0, first_n = 0;  // the first segment's window (one_pass)
-  if (one_pass) {
-    const uint64_t hit =
-        __builtin_amdgcn_ballot_w64(lane < a.batch && (int64_t)NKV * lane_incl > x0);
-    const int f = __builtin_ctzll(hit);  // x0 < TT: some lane hits
-    const int Uf = __builtin_amdgcn_readlane(lane_U, f);
-    sp = {f, (int64_t)NKV * (__builtin_amdgcn_readlane(lane_incl, f) - Uf), Uf};
-    first_T = __builtin_amdgcn_readlane(lane_T, f);
-    first_ov = __builtin_amdgcn_readlane(lane_ov, f);
-    first_n = __builtin_amdgcn_readlane(lane_n, f);
-  } else {
-    sp = locate(g, a, x0, lane);
-  }
-  bool first_seg = one_pass;
   int kvh = (int)((x0 - sp.start) / sp.units);
   int u = (int)((x0 - sp.start) % sp.units);  // unit offset inside the segment
   int64_t x = x0;
@@ -1455,6 +1490,103 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     if (cut_last >= 0)
       __hip_atomic_store(a.ws_flag + cut_last, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  return t_first;
+}
+
+
+
+// The per-query kernels (PQ) keep one more run's state live across their run
+// loop, which at three waves per SIMD spills; they run with the register
+// budget of two (the v1 symbols decode one sequence, or the causal prefixes
+// of one, far from filling the device).
+template <int HD, int P, bool PACK, bool PQ>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
+    PQ ? 1 : min_waves_per_simd<HD, PACK>()))) void kivi_decode_stream_kernel(KiviGeo g,
+                                                                              DecodeArgs a) {
+  constexpr int S = stages<HD, PACK>();
+  static_assert(S >= 2 && S <= 4, "wait_stages covers up to 3 stages in flight");
+  __shared__ __attribute__((aligned(16))) StageBuf<HD> ring[S];
+  // Q rows of the current segment, one per MFMA column head (rows past G stay zero)
+  // Q rows padded by 16 bytes: at a 2 HD-byte stride (a multiple of the 256
+  // bytes the LDS banks span) the rows' k-step reads would all hit the same
+  // banks, an 8-way conflict on every read
+  constexpr int QROW = HD + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t qrows[(PACK ? 8 : 16) * QROW];
+
+  const int lane = threadIdx.x;
+  const uint64_t t_start = a.stamps ? __builtin_amdgcn_s_memrealtime() : 0;
+  if ((int)blockIdx.x >= a.waves) {
+    merge_segments<HD, PACK, PQ>(g, a, lane);
+    write_stamp(a, t_start, 0, lane);
+    return;
+  }
+  if constexpr (PQ) {
+    const Nibble nb;
+    // the ones block of every stage (the DMAs never write it)
+    if (lane < 32) {
+#pragma unroll
+      for (int s_ = 0; s_ < S; ++s_) ((uint32_t*)ring[s_].ones)[lane] = 0x3C003C00u;
+    }
+    // rows past G are read as zeros by the columns that carry no head
+    for (int i = lane; i < (int)(sizeof(qrows) / 16); i += 64)
+      ((u32x4*)qrows)[i] = u32x4{0u, 0u, 0u, 0u};
+    const float sscale = 1.4426950408889634f / __builtin_sqrtf((float)HD);  // log2(e)/sqrt(HD)
+    for (int64_t r = blockIdx.x;; r += a.waves) {
+      const RunLoc rl = locate_run(g, a, r, lane);
+      if (rl.q < 0) break;
+      const int64_t TTq = (int64_t)g.nkv * rl.units, wl = r - rl.r0;
+      const int64_t x0 = wl * TTq / rl.runs, x1 = (wl + 1) * TTq / rl.runs;
+      if (x0 >= x1) continue;
+      stream_run<HD, P, PACK>(g, a, ring, qrows, nb, sscale, lane, x0, x1,
+                              SeqSpan{rl.q, 0, rl.units}, false, 0, 0, 0, (int)r);
+    }
+    return;
+  }
+  const int G = g.gqa, NKV = g.nkv;
+  // Up to 64 sequences, one length load per lane serves the stream's total,
+  // the run's first sequence and that sequence's window: the first block-table
+  // read waits for one memory round, not three.
+  const bool one_pass = a.batch <= 64;
+  int lane_T = 0, lane_ov = 0, lane_n = 0, lane_U = 0;
+  if (one_pass && lane < a.batch) {
+    lane_T = seq_tiles(g, a, lane, &lane_ov, &lane_n);
+    lane_U = lane_ov / kGroup + kResidualUnits * (lane_T - lane_ov / kGroup);
+  }
+  const int lane_incl = wave_incl_scan(lane_U, lane);
+  const int64_t TT = one_pass ? (int64_t)NKV * __builtin_amdgcn_readlane(lane_incl, 63)
+                              : stream_units(g, a, lane);
+  const int64_t W = stream_waves(TT, a.waves);
+  const int w = blockIdx.x;
+  if (w >= W) return;
+  const int64_t x0 = (int64_t)w * TT / W, x1 = (int64_t)(w + 1) * TT / W;
+  if (x0 >= x1) return;
+
+  const Nibble nb;
+  // the ones block of every stage (the DMAs never write it)
+  if (lane < 32) {
+#pragma unroll
+    for (int s_ = 0; s_ < S; ++s_) ((uint32_t*)ring[s_].ones)[lane] = 0x3C003C00u;
+  }
+  // rows past G are read as zeros by the columns that carry no head
+  for (int i = lane; i < (int)(sizeof(qrows) / 16); i += 64) ((u32x4*)qrows)[i] = u32x4{0u, 0u, 0u, 0u};
+  const float sscale = 1.4426950408889634f / __builtin_sqrtf((float)HD);  // log2(e)/sqrt(HD)
+
+  SeqSpan sp;
+  int first_T = 0, first_ov = 0, first_n = 0;  // the first segment's window (one_pass)
+  if (one_pass) {
+    const uint64_t hit =
+        __builtin_amdgcn_ballot_w64(lane < a.batch && (int64_t)NKV * lane_incl > x0);
+    const int f = __builtin_ctzll(hit);  // x0 < TT: some lane hits
+    const int Uf = __builtin_amdgcn_readlane(lane_U, f);
+    sp = {f, (int64_t)NKV * (__builtin_amdgcn_readlane(lane_incl, f) - Uf), Uf};
+    first_T = __builtin_amdgcn_readlane(lane_T, f);
+    first_ov = __builtin_amdgcn_readlane(lane_ov, f);
+    first_n = __builtin_amdgcn_readlane(lane_n, f);
+  } else {
+    sp = locate(g, a, x0, lane);
+  }
+  const uint64_t t_first = stream_run<HD, P, PACK>(g, a, ring, qrows, nb, sscale, lane, x0, x1, sp,
+                                                   one_pass, first_T, first_ov, first_n, w);
   // profiling: the run's units (bits 0-31) and the ticks to its first group (32-63)
   write_stamp(a, t_start, (uint64_t)(x1 - x0) | ((t_first ? t_first - t_start : 0) << 32), lane);
 }
@@ -1463,12 +1595,18 @@ template <int HD, int P>
 static void launch_one(const KiviGeo& g, const DecodeArgs& a, hipStream_t stream,
                        hipEvent_t start, hipEvent_t stop) {
   const dim3 grid(a.waves + a.merge_wgs);
-  if (g.gqa <= 8)
-    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, true>), grid, dim3(64), 0, stream,
-                          start, stop, 0, g, a);
+  if (g.gqa <= 8 && a.per_query)
+    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, true, true>), grid, dim3(64), 0,
+                          stream, start, stop, 0, g, a);
+  else if (g.gqa <= 8)
+    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, true, false>), grid, dim3(64), 0,
+                          stream, start, stop, 0, g, a);
+  else if (a.per_query)
+    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, false, true>), grid, dim3(64), 0,
+                          stream, start, stop, 0, g, a);
   else
-    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, false>), grid, dim3(64), 0, stream,
-                          start, stop, 0, g, a);
+    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, false, false>), grid, dim3(64), 0,
+                          stream, start, stop, 0, g, a);
 }
 
 hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& args, int batch,
@@ -1524,7 +1662,7 @@ static int resident_per_cu() {
   static int n = 0;
   if (n == 0) {
     int k = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, kivi_decode_stream_kernel<HD, P, PACK>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, kivi_decode_stream_kernel<HD, P, PACK, false>,
                                                      64, 0) != hipSuccess ||
         k < 1)
       k = 8;

@@ -57,6 +57,8 @@ struct DecodeArgs {
   uint64_t merge_skew = 0;     // matrix-core kernel: 0; 1 only in the forced-timeout test
   int retained_pages = -1;  // >= 0: sparse-retained window (compact block table)
   uint32_t* status = nullptr;  // matrix-core kernel: set to 1 when a merge wait runs out
+  uint64_t* ws_poison = nullptr;  // matrix-core kernel: the workspace's poison word
+  int per_query = 0;  // matrix-core kernel: cut each query's streams by its own length alone
 };
 
 // Decode window of one sequence.  Dense: the split rule (decode_window).

@@ -148,6 +148,10 @@ def lib() -> ctypes.CDLL:
     L.jacq_kivi_init.restype = ctypes.c_int
     L.jacq_kivi_decode_status.argtypes = [_vp, ctypes.c_size_t, _vp]
     L.jacq_kivi_decode_status.restype = ctypes.c_int
+    L.jacq_kivi_release_workspaces.argtypes = []
+    L.jacq_kivi_release_workspaces.restype = ctypes.c_int
+    L.jacq_kivi_test_device_allocations.argtypes = []
+    L.jacq_kivi_test_device_allocations.restype = ctypes.c_int64
     L.jacq_kivi_test_force_merge_timeout.argtypes = [ctypes.c_uint32]
     L.jacq_kivi_test_force_merge_timeout.restype = None
     L.jacq_kivi_profile_wave_stamps.argtypes = [_vp, _i32]

@@ -221,16 +221,21 @@ def test_v1_jac_launch_all_boundaries(kivi):
 
 
 def test_v1_batched_decode_equals_single(kivi):
-    """jac_launch_batched matches jac_launch per query (variants.rs:1207-1215)."""
-    st = State(V1, lens=[1000], seed=8)
+    """jac_launch_batched equals jac_launch per query bit for bit
+    (variants.rs:1211-1213): the v1 symbols cut each query's work by its own
+    length alone.  60 causal queries up to the 4096-token v1 maximum need
+    more than one launch of the static workspace region, which must not
+    change any query's bits either."""
+    st = State(V1, lens=[4096], seed=8)
     st.build_oracle()
     g = to_torch(st)
     bt = torch.from_numpy(st.tables[0]).cuda()
     pool = [g[n] for n in ("k_code", "k_scale", "k_zero", "v_code", "v_scale", "v_zero")]
-    nq = 20
+    nq = 60
     rng = np.random.default_rng(3)
     qs = rng.standard_normal((nq, 40, 128)).astype(np.float16)
-    seq = np.arange(1000 - nq + 1, 1001).astype(np.int32)
+    seq = np.arange(4096 - nq + 1, 4097).astype(np.int32)
+    seq[:5] = [1, 128, 129, 160, 1000]  # short and boundary queries in the same call
     qt = torch.from_numpy(qs).cuda()
     out_b = torch.empty((nq, 40, 128), dtype=torch.float32, device="cuda")
     kivi.kivi_decode_batched_dsl(qt, torch.from_numpy(seq).cuda(), bt, *pool, g["k_scr"][0],
@@ -240,14 +245,45 @@ def test_v1_batched_decode_equals_single(kivi):
         kivi.kivi_decode_dsl(qt[i].contiguous(), bt, *pool, g["k_scr"][0], g["v_scr"][0],
                              int(seq[i]), out)
         torch.cuda.synchronize()
-        # one sequence decoded alone or inside a batch: the work split differs,
-        # so the softmax rescale points and with them the fp16 rounding of P
-        # (2^-11 relative) differ: the two agree to that rounding, not bit for bit
-        d = (out - out_b[i]).abs()
-        assert torch.allclose(out, out_b[i], atol=1e-3, rtol=2e-3), \
-            f"query {i}: max diff {d.max().item():.3e}, rel {(d / out_b[i].abs().clamp_min(1e-3)).max().item():.3e}"
-        ref = o.decode_twopass(st.cache, 0, qs[i].view(np.uint16), st.tables[0], int(seq[i]))
-        assert_close(out.cpu().numpy(), ref, f"batched q{i}")
+        assert torch.equal(out.view(torch.int32), out_b[i].view(torch.int32)), \
+            f"query {i} (seq_len {seq[i]}): max diff {(out - out_b[i]).abs().max().item():.3e}"
+        if i < 8 or i % 13 == 0:
+            ref = o.decode_twopass(st.cache, 0, qs[i].view(np.uint16), st.tables[0], int(seq[i]))
+            assert_close(out.cpu().numpy(), ref, f"batched q{i}")
+
+
+def test_v1_decode_allocates_nothing_under_capture(kivi):
+    """The v1 decode symbols allocate nothing (the reference's contract: every
+    buffer is the caller's, source_patch.py:2391-2417).  The first v1 decode
+    on a fresh stream is captured into a graph; the library's allocation count
+    does not move, and every replay equals the eager decode bit for bit."""
+    st = State(V1, lens=[4096], seed=12)
+    st.build_oracle()
+    g = to_torch(st)
+    bt = torch.from_numpy(st.tables[0]).cuda()
+    pool = [g[n] for n in ("k_code", "k_scale", "k_zero", "v_code", "v_scale", "v_zero")]
+    kivi.lib().jacq_kivi_init()
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    qs = [torch.randn((40, 128), generator=gen, device="cuda").half() for _ in range(3)]
+    q_in = qs[0].clone()
+    out = torch.empty((40, 128), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    before = kivi.lib().jacq_kivi_test_device_allocations()
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        kivi.kivi_decode_dsl(q_in, bt, *pool, g["k_scr"][0], g["v_scr"][0], 3000, out)
+    for i, q in enumerate(qs * 2):
+        q_in.copy_(q)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = torch.empty_like(out)
+        kivi.kivi_decode_dsl(q, bt, *pool, g["k_scr"][0], g["v_scr"][0], 3000, ref)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), f"replay {i}"
+    assert kivi.lib().jacq_kivi_test_device_allocations() == before
+    refn = o.decode_twopass(st.cache, 0, _np(qs[-1]), st.tables[0], 3000)
+    assert_close(out.cpu().numpy(), refn, "captured jac_launch")
 
 
 def test_page16_equals_page32(kivi):
@@ -666,6 +702,58 @@ def test_merge_timeout_drains_and_is_reported(kivi):
     out = cache.decode(q, lens, bt)
     torch.cuda.synchronize()
     assert_close(out.cpu().numpy(), ref, "decode after the reset")
+
+
+def test_merge_timeout_poisons_graph_replays(kivi):
+    """A graph replay never passes through the host's status check, and it
+    repeats its launch epoch: after a merge on its workspace timed out, flags
+    that the late stream wavefronts stored would look like the replay's own.
+    The timed-out merge poisons the workspace, so the replays' merged segments
+    are NaN -- never finite values built from stale partials -- until
+    jacq_kivi_decode_status zeroes the workspace; then replays equal the
+    eager decode again."""
+    w = wl.WORKLOADS["qwen14b"]
+    st = State(w, lens=[3000, 129, 20, 700, 1], seed=17)
+    st.build_oracle()
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, st.max_pages,
+                            st.num_pages)
+    cache = kivi.PagedKiviCache.from_tensors(geo, to_torch(st))
+    q = torch.from_numpy(st.q).view(torch.float16).cuda()
+    lens = torch.from_numpy(st.lens.astype(np.int32)).cuda()
+    bt = torch.from_numpy(st.tables).cuda()
+    ref = st.decode_ref()
+    kivi.decode_status()
+    nbytes = kivi.lib().jacq_kivi_decode_workspace_size(ctypes_geo(kivi, geo), st.batch)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    out = torch.empty((st.batch, w.nh, w.hd), dtype=torch.float32, device="cuda")
+    eager = cache.decode(q, lens, bt, out=torch.empty_like(out), workspace=ws)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cache.decode(q, lens, bt, out=out, workspace=ws)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int32), eager.view(torch.int32))
+    # an eager decode on the same workspace times out (forced from the host)
+    kivi.lib().jacq_kivi_test_force_merge_timeout(20)
+    try:
+        cache.decode(q, lens, bt, out=torch.empty_like(out), workspace=ws)
+        torch.cuda.synchronize()
+    finally:
+        kivi.lib().jacq_kivi_test_force_merge_timeout(0)
+    for i in range(2):  # no jacq_kivi_decode_status in between
+        out.fill_(5.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        counts = _segment_counts(w, out.cpu().numpy().astype(np.float64), ref)
+        assert counts["other"] == 0 and counts["nan"] >= 1 and counts["match"] >= 1, (i, counts)
+    with pytest.raises(kivi.KiviMergeTimeout, match="reset"):
+        kivi.decode_status(ws)
+    for i in range(2):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), eager.view(torch.int32)), f"replay {i} after reset"
+    kivi.decode_status()
 
 
 def test_merge_timeout_exits_v1_symbols(kivi):

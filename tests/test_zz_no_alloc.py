@@ -1,7 +1,8 @@
 """jacq_kivi_decode_noalloc (the decode that allocates nothing; its split-K
 workspace is the library's static device array) against jacq_kivi_decode
 through the C ABI: bit-identical outputs on two calls in a row, the second
-with a smaller batch, plus the size limit and the set-up requirement."""
+with a smaller batch, plus the size limit and the set-up requirement (a call
+before jacq_kivi_init is refused, checked in a fresh child process)."""
 from __future__ import annotations
 
 import ctypes
@@ -82,3 +83,17 @@ def test_noalloc_rejects_batches_beyond_the_static_array(kivi):
     assert "static" in kivi.last_error() and str(need) in kivi.last_error()
     torch.cuda.synchronize()
     assert bool((out == 3.0).all())
+
+
+def test_noalloc_before_init_is_refused():
+    """jacq_kivi_decode_noalloc before jacq_kivi_init on the device returns
+    JACQ_KIVI_EINVAL naming jacq_kivi_init and launches nothing (a fresh
+    child process, tests/noalloc_before_init_check.py, in which no entry
+    point has run)."""
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    r = subprocess.run([sys.executable, os.path.join(here, "noalloc_before_init_check.py")],
+                       capture_output=True, text=True, timeout=100)
+    assert r.returncode == 0 and "REFUSED_OK" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]
