@@ -294,6 +294,32 @@ int jacq_kivi_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q,
                      const jacq_half_t* V_RESIDUAL_SCRATCH, int32_t batch, float* O,
                      void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* One decode step of the cache in one launch: append one token per sequence
+ * (quantising the 32-token group that ages out of the residual window where
+ * one does, and shifting the scratch), then decode one query per sequence
+ * over the new state.  It replaces the reference's per-token pair
+ * kivi_cache_write(SEQ_LEN) followed by kivi_decode(SEQ_LEN) on one stream
+ * (integrations/vllm_kivi/source_patch.py:3259-3288; the writer :1661-1697,
+ * the decode as jacq_kivi_decode) and leaves pages, scales, zeros and the
+ * scratch bit for bit as jacq_kivi_cache_append(START_LENS = SEQ_LENS - 1,
+ * num_new = 1) would, and O as jacq_kivi_decode(SEQ_LENS) on that state
+ * computes it (the same kernel, to its run split).
+ *   NEW_K, NEW_V  [batch, NKV, HD] fp16, the token at position SEQ_LENS - 1
+ *   SEQ_LENS      [batch] int32 (device), lengths after the write, >= 1
+ *   pages and scratch are written in place (jacq_kivi_cache_append's arrays)
+ * workspace: NULL or at least jacq_kivi_write_decode_workspace_size bytes,
+ * contents on entry irrelevant (as jacq_kivi_decode's). */
+size_t jacq_kivi_write_decode_workspace_size(const jacq_kivi_geometry* geo, int32_t batch);
+int jacq_kivi_write_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q,
+                           const jacq_half_t* NEW_K, const jacq_half_t* NEW_V,
+                           const int32_t* SEQ_LENS, const int32_t* BLOCK_TABLES,
+                           uint8_t* K_CODE_PAGES, jacq_half_t* K_SCALE_PAGES,
+                           jacq_half_t* K_ZERO_PAGES, uint8_t* V_CODE_PAGES,
+                           jacq_half_t* V_SCALE_PAGES, jacq_half_t* V_ZERO_PAGES,
+                           jacq_half_t* K_RESIDUAL_SCRATCH, jacq_half_t* V_RESIDUAL_SCRATCH,
+                           int32_t batch, float* O, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream);
+
 /* jacq_kivi_decode with no allocation at all.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

@@ -346,6 +346,16 @@ void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& 
   a.ws_flag = ws ? (uint64_t*)(a.ws_acc + slots * g.hd) : nullptr;
 }
 
+// Fused write + decode: writer wavefronts at the front of the grid (about one
+// per 16 (sequence, kv head, K | V) items, at most 64), and one epoch flag per
+// item after the split-K workspace.
+int step_writer_waves(const KiviGeo& g, int batch) {
+  return std::max(1, std::min(64, 2 * batch * g.nkv / 16));
+}
+size_t step_flag_bytes(const KiviGeo& g, int batch) {
+  return (size_t)2 * batch * g.nkv * sizeof(uint64_t);
+}
+
 // ---- measurement hook: HIP events around the decode ----
 // While enabled, each decode call takes the next triple of a pre-created
 // event pool and uses it on the call's own stream: before the decode, a
@@ -397,7 +407,7 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
                const jacq_half_t* vsc, const jacq_half_t* vz, const jacq_half_t* kscr,
                const jacq_half_t* vscr, int64_t scr_stride, int batch, float* O, void* ws,
                size_t ws_bytes, hipStream_t stream, int retained_pages = -1,
-               bool per_query = false) {
+               bool per_query = false, const jacq::AppendArgs* step = nullptr) {
   if (!aligned16({Q, O, kc, ksc, kz, vc, vsc, vz, kscr, vscr, ws}))
     return fail(JACQ_KIVI_EINVAL, "tensor and workspace pointers must be 16-byte aligned");
   const KiviGeo g = make_geo(x);
@@ -411,10 +421,11 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
     jacq::window_of(g, retained_pages, seq_len_host, &ov, &rv);
     max_tokens = ov + rv;
   }
-  const int waves = jacq::decode_stream_waves(g, ds.cus);
+  const int nw = step ? step_writer_waves(g, batch) : 0;
+  const int waves = jacq::decode_stream_waves(g, ds.cus) - nw;
   const SplitPlan sp =
       per_query ? plan_splits_per_query(g, max_tokens, waves) : plan_splits(max_tokens);
-  const size_t need = workspace_bytes(g, batch, sp, waves);
+  const size_t need = workspace_bytes(g, batch, sp, waves) + (step ? step_flag_bytes(g, batch) : 0);
   if (need > 0) {
     if (ws == nullptr) {
       // sized for at least kLibraryWorkspaceBatch sequences on first use, so
@@ -450,6 +461,12 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
   a.retained_pages = retained_pages;
   a.status = ds.status_dev;
   fill_ws(a, g, batch, sp, waves, need > 0 ? ws : nullptr);
+  if (step) {
+    a.wr = *step;
+    a.writer_waves = nw;
+    // the writer flags follow the split-K workspace
+    a.ws_wflag = (uint64_t*)((uint8_t*)ws + (need - step_flag_bytes(g, batch)));
+  }
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   profile_slot(ev);
   hipError_t e;
@@ -674,6 +691,60 @@ int jacq_kivi_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q, const 
                     K_SCALE_PAGES, K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES,
                     K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, scr, batch, O, workspace,
                     workspace_bytes_, stream);
+}
+
+size_t jacq_kivi_write_decode_workspace_size(const jacq_kivi_geometry* geo, int32_t batch) {
+  if (check_geometry(geo) != JACQ_KIVI_OK || batch < 1) return 0;
+  int dev = 0;
+  if (current_device(&dev) != JACQ_KIVI_OK) return 0;
+  const KiviGeo g = make_geo(*geo);
+  const int waves = jacq::decode_stream_waves(g, device_state(dev).cus) -
+                    step_writer_waves(g, batch);
+  return workspace_bytes(g, batch, plan_splits(max_seq_len(*geo)), waves) +
+         step_flag_bytes(g, batch);
+}
+
+int jacq_kivi_write_decode(const jacq_kivi_geometry* geo, const jacq_half_t* Q,
+                           const jacq_half_t* NEW_K, const jacq_half_t* NEW_V,
+                           const int32_t* SEQ_LENS, const int32_t* BLOCK_TABLES,
+                           uint8_t* K_CODE_PAGES, jacq_half_t* K_SCALE_PAGES,
+                           jacq_half_t* K_ZERO_PAGES, uint8_t* V_CODE_PAGES,
+                           jacq_half_t* V_SCALE_PAGES, jacq_half_t* V_ZERO_PAGES,
+                           jacq_half_t* K_RESIDUAL_SCRATCH, jacq_half_t* V_RESIDUAL_SCRATCH,
+                           int32_t batch, float* O, void* workspace, size_t workspace_bytes_,
+                           hipStream_t stream) {
+  if (int e = check_geometry(geo)) return e;
+  if (batch < 1) return fail(JACQ_KIVI_EINVAL, "batch must be >= 1");
+  if (!Q || !NEW_K || !NEW_V || !SEQ_LENS || !K_CODE_PAGES || !K_SCALE_PAGES || !K_ZERO_PAGES ||
+      !V_CODE_PAGES || !V_SCALE_PAGES || !V_ZERO_PAGES || !K_RESIDUAL_SCRATCH ||
+      !V_RESIDUAL_SCRATCH || !O || (!BLOCK_TABLES && geo->max_pages_per_seq > 0))
+    return fail(JACQ_KIVI_EINVAL, "null tensor pointer");
+  if (!aligned16({NEW_K, NEW_V}))
+    return fail(JACQ_KIVI_EINVAL, "tensor pointers must be 16-byte aligned");
+  const int64_t scr = (int64_t)geo->num_kv_heads * (geo->residual + geo->group_size) * geo->head_dim;
+  jacq::AppendArgs w{};
+  w.k_code = K_CODE_PAGES;
+  w.k_scale = K_SCALE_PAGES;
+  w.k_zero = K_ZERO_PAGES;
+  w.v_code = V_CODE_PAGES;
+  w.v_scale = V_SCALE_PAGES;
+  w.v_zero = V_ZERO_PAGES;
+  w.k_scr = K_RESIDUAL_SCRATCH;
+  w.v_scr = V_RESIDUAL_SCRATCH;
+  w.scr_stride = scr;
+  w.new_k = NEW_K;
+  w.new_v = NEW_V;
+  w.new_stride = (int64_t)geo->num_kv_heads * geo->head_dim;
+  w.block_tables = BLOCK_TABLES;
+  w.bt_stride = geo->max_pages_per_seq;
+  w.start_lens = nullptr;  // SEQ_LENS - 1, read by the kernel
+  w.num_new = 1;
+  if (use_simple_decode())
+    return fail(JACQ_KIVI_EINVAL, "the fused write + decode runs on the matrix-core decode only");
+  return run_decode(*geo, Q, SEQ_LENS, -1, BLOCK_TABLES, geo->max_pages_per_seq, K_CODE_PAGES,
+                    K_SCALE_PAGES, K_ZERO_PAGES, V_CODE_PAGES, V_SCALE_PAGES, V_ZERO_PAGES,
+                    K_RESIDUAL_SCRATCH, V_RESIDUAL_SCRATCH, scr, batch, O, workspace,
+                    workspace_bytes_, stream, -1, false, &w);
 }
 
 int jacq_kivi_decode_noalloc(const jacq_kivi_geometry* geo, const jacq_half_t* Q,

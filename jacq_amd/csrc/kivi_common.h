@@ -77,6 +77,38 @@ __host__ __device__ inline void split_plan(int n, int* nsplit, int* chunk) {
   *nsplit = n > 0 ? (n + c - 1) / c : 1;
 }
 
+// ---- quantiser arithmetic shared by the writer and the fused step ----
+// static_cast<int>(rintf(x)) clamped to [0, 15] (source_patch.py:1517-1522),
+// with the conversion CUDA and gfx950 hardware perform: out-of-range values
+// saturate, NaN becomes 0.  Clamped in the float domain, because an
+// out-of-range float -> int conversion is undefined in C++ and the compiler
+// may assume it does not happen.
+__device__ inline int clamp_code(float x) {
+  const float r = __builtin_rintf(x);
+  if (r >= 15.0f) return 15;
+  if (r >= 0.0f) return (int)r;
+  return 0;  // negative or NaN
+}
+
+// fminf / fmaxf of the reference's age-out kernels (source_patch.py:1555-1558,
+// :1598-1599): a NaN operand is dropped, NaN results only when both are NaN.
+// For a +0 / -0 pair, min gives -0 and max +0 (C Annex F's recommendation;
+// LLVM's minnum leaves it open, so it is written out).  Both are then
+// commutative and associative: the partial reductions below may merge in any
+// order and still give one sequential loop's bits.
+__device__ inline float min_num(float a, float b) {
+  if (b != b) return a;
+  if (a != a) return b;
+  if (a == b) return __uint_as_float(__float_as_uint(a) | __float_as_uint(b));
+  return b < a ? b : a;
+}
+__device__ inline float max_num(float a, float b) {
+  if (b != b) return a;
+  if (a != a) return b;
+  if (a == b) return __uint_as_float(__float_as_uint(a) & __float_as_uint(b));
+  return b > a ? b : a;
+}
+
 __device__ inline float h2f(uint16_t h) {
   _Float16 v = __builtin_bit_cast(_Float16, h);
   return (float)v;

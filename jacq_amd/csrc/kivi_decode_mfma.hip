@@ -847,9 +847,11 @@ struct ResTile {
   vrow_t vr[8];
 };
 
-template <int HD>
+// FUSED: residual row new_row (>= 0) is the step's new token, read from
+// NEW_K / NEW_V.
+template <int HD, bool FUSED>
 __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, int b, int h,
-                                       int ov, int n, int tile, int lane) {
+                                       int ov, int n, int tile, int lane, int new_row) {
   constexpr int KS = HD / 32, CPL = HD / 16;
   // lane offsets from an opaque copy of the lane id: hoisted out of the
   // loops they would hold 64-bit registers through the whole run
@@ -860,11 +862,24 @@ __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, in
   const int t0 = tile * kGroup;
   const int tn = min(kGroup, n - t0);
   const int r0 = t0 - ov;  // scratch row of token t0
+  // the row pointers of K and V (FUSED: the new token's row from NEW_K / NEW_V)
+  auto krow = [&](int row) -> const uint16_t* {
+    if constexpr (FUSED) {
+      if (row == new_row) return a.wr.new_k + (int64_t)b * a.wr.new_stride + (int64_t)h * HD;
+    }
+    return kscr + (int64_t)row * HD;
+  };
+  auto vrow = [&](int row) -> const uint16_t* {
+    if constexpr (FUSED) {
+      if (row == new_row) return a.wr.new_v + (int64_t)b * a.wr.new_stride + (int64_t)h * HD;
+    }
+    return vscr + (int64_t)row * HD;
+  };
   ResTile<HD> rt;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     const int tl = 8 * (c >> 2) + 4 * tt + (c & 3);
-    const uint16_t* kr = kscr + (int64_t)(r0 + (tl < tn ? tl : 0)) * HD + j * (HD / 4);
+    const uint16_t* kr = krow(r0 + (tl < tn ? tl : 0)) + j * (HD / 4);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       rt.kv[tt][ks] = __builtin_nontemporal_load((const u32x4*)(kr + 8 * ks));
@@ -872,8 +887,8 @@ __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, in
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
     const int tl = 8 * j + r;
-    rt.vr[r] = __builtin_nontemporal_load((const typename ResTile<HD>::vrow_t*)(
-        vscr + (int64_t)(r0 + (tl < tn ? tl : 0)) * HD + CPL * c));
+    rt.vr[r] = __builtin_nontemporal_load(
+        (const typename ResTile<HD>::vrow_t*)(vrow(r0 + (tl < tn ? tl : 0)) + CPL * c));
   }
   return rt;
 }
@@ -929,6 +944,16 @@ __device__ inline int64_t query_run_start(const KiviGeo& g, const DecodeArgs& a,
     run += __builtin_amdgcn_readfirstlane(wave_sum_i(R));
   }
   return run;
+}
+
+// The step's sequence b ages a group out: its old-token count grows.
+__device__ inline bool step_ages(const KiviGeo& g, int len_after) {
+  return len_after >= 1 &&
+         split_old_tokens(len_after, g.residual) > split_old_tokens(len_after - 1, g.residual);
+}
+
+__device__ inline int step_len(const DecodeArgs& a, int b) {
+  return ((const __attribute__((address_space(4))) int32_t*)a.seq_lens)[b];
 }
 
 // ---- split-K merge, run by workgroups of the same launch ----
@@ -1038,8 +1063,9 @@ __device__ inline void write_stamp(const DecodeArgs& a, uint64_t t0, uint64_t in
 // likewise, O = acc / max(L, 1e-30), in the log2 domain of the decode loop.
 // The pieces of a segment are recomputed from the same split the stream
 // wavefronts used; a segment with a single non-empty piece was written whole.
-template <int HD, bool PACK, bool PQ>
-__device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) {
+template <int HD, bool PACK, bool PQ, bool FUSED>
+__device__ __attribute__((always_inline)) inline void merge_segments(const KiviGeo& g,
+                                                                   const DecodeArgs& a, int lane) {
   constexpr int K = (PACK ? 8 : 16) * HD / 256;  // float4 outputs per lane: G * HD <= 256 K
   constexpr int U = K <= 2 ? 8 : K > 4 ? 1 : 2;  // partials whose loads are in flight together
   const int G = g.gqa, NKV = g.nkv, n4 = G * HD / 4;
@@ -1063,7 +1089,7 @@ __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) 
     gi[k] = 4 * e / HD;
     d[k] = 4 * e - gi[k] * HD;
   }
-  for (int seg = (int)blockIdx.x - a.waves; seg < nseg; seg += a.merge_wgs) {
+  for (int seg = (int)blockIdx.x - a.writer_waves - a.waves; seg < nseg; seg += a.merge_wgs) {
     const int b = seg / NKV, h = seg - b * NKV;
     int ov, n;
     const int T = seq_tiles(g, a, b, &ov, &n);
@@ -1189,6 +1215,15 @@ __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) 
       if (on[k])
         *(floatx4*)(out + (int64_t)gi[k] * HD + d[k]) =
             late ? floatx4{NAN, NAN, NAN, NAN} : acc[k] / fmaxf(Lsum[k], 1.0e-30f);
+    // fused step: every piece of the segment has landed, so its readers of
+    // the writer's age-out are done; its flags start the next launch at zero
+    if constexpr (FUSED) {
+      if (lane == 0 && step_ages(g, step_len(a, b))) {
+        uint64_t* f = a.ws_wflag + 2 * (int64_t)seg;
+        __hip_atomic_store(f, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(f + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
   // a wait ran out (or an earlier one poisoned the workspace): the workspace
   // stays poisoned, and the host sees it in the device's status word
@@ -1199,12 +1234,202 @@ __device__ void merge_segments(const KiviGeo& g, const DecodeArgs& a, int lane) 
   }
 }
 
+// ---- fused write + decode: the writer wavefronts ----
+//
+// jacq_kivi_write_decode appends one token per sequence (length seq_lens - 1
+// before, seq_lens after) and decodes the new state in one launch.  The
+// writer's work rides on a few wavefronts at the front of the grid, which are
+// dispatched before any decode wavefront and wait for nothing:
+//  - a plain append stores the new token in scratch row r0.  No decode
+//    wavefront of this launch reads that row from the scratch: the residual
+//    tile that holds it takes the row from NEW_K / NEW_V instead;
+//  - a sequence that ages a group out (its 32 oldest scratch rows become int4
+//    pages) is one item per (kv head, K or V): quantise rows 0..31 into the
+//    group's pages, shift the scratch down 32 rows, store the new token in
+//    rows R - 1 and r0 (the writer's final state, stale copy included), then
+//    a release fence and the launch's epoch in the item's flag.  Decode
+//    wavefronts that read the new group or the residual tiles of such a
+//    segment wait for both of its flags (and acquire) before their first load
+//    of them; the wavefront or merge that finishes the segment clears them.
+// The arithmetic is the writer kernel's (kivi_append_kernel), so pages and
+// scratch end bit for bit as a separate write would leave them.
+
+template <int HD>
+__device__ __attribute__((always_inline)) inline void step_age_out(const KiviGeo& g, const DecodeArgs& a,
+                                                        int b, int h, bool is_v, int lane) {
+#pragma clang fp contract(off)
+  constexpr int HDP = HD / 2, HDG = HD / kGroup;
+  const AppendArgs& w = a.wr;
+  const int P = g.page, ppg = kGroup / P;
+  const int start = step_len(a, b) - 1;
+  const int old0 = split_old_tokens(start, g.residual), r0 = start - old0;  // r0 = R + 31
+  uint16_t* xs = (is_v ? w.v_scr : w.k_scr) + (int64_t)b * w.scr_stride + (int64_t)h * g.rs * HD;
+  const uint16_t* nx = (is_v ? w.new_v : w.new_k) + (int64_t)b * w.new_stride + (int64_t)h * HD;
+  const int fp = (old0 / kGroup) * ppg;  // the group's first logical page
+  const bool table_ok = fp + ppg <= g.max_pages;
+  int p0 = -1, p1 = -1;
+  if (table_ok) {
+    const int32_t* bt = w.block_tables + (int64_t)b * w.bt_stride;
+    p0 = bt[fp];
+    p1 = ppg == 2 ? bt[fp + 1] : p0;
+  }
+  auto phys_ok = [&](int p) { return p >= 0 && p < g.num_pages; };
+  if (!is_v) {
+    // K: lane = channel pair (2 lane, 2 lane + 1), all 32 tokens
+    if (lane < HDP) {
+      uint32_t x[kGroup];
+#pragma unroll
+      for (int t = 0; t < kGroup; ++t) x[t] = *(const uint32_t*)(xs + t * HD + 2 * lane);
+      float mn0 = h2f((uint16_t)x[0]), mx0 = mn0, mn1 = h2f((uint16_t)(x[0] >> 16)), mx1 = mn1;
+#pragma unroll
+      for (int t = 1; t < kGroup; ++t) {
+        const float v0 = h2f((uint16_t)x[t]), v1 = h2f((uint16_t)(x[t] >> 16));
+        mn0 = min_num(mn0, v0);
+        mx0 = max_num(mx0, v0);
+        mn1 = min_num(mn1, v1);
+        mx1 = max_num(mx1, v1);
+      }
+      float s0 = (mx0 - mn0) / 15.0f, s1 = (mx1 - mn1) / 15.0f;
+      if (!(s0 > 0.0f)) s0 = 1.0f;
+      if (!(s1 > 0.0f)) s1 = 1.0f;
+      if (table_ok) {
+        const uint32_t sc = (uint32_t)f2h(s0) | ((uint32_t)f2h(s1) << 16);
+        const uint32_t zr = (uint32_t)f2h(mn0) | ((uint32_t)f2h(mn1) << 16);
+        for (int pg = 0; pg < ppg; ++pg) {  // K scales live in every page of the group
+          const int phys = pg == 0 ? p0 : p1;
+          if (!phys_ok(phys)) continue;
+          const int64_t base = ((int64_t)phys * g.nkv + h) * HD + 2 * lane;
+          *(uint32_t*)(w.k_scale + base) = sc;
+          *(uint32_t*)(w.k_zero + base) = zr;
+        }
+#pragma unroll
+        for (int t = 0; t < kGroup; ++t) {
+          const int phys = t < P ? p0 : p1;
+          const int c0 = clamp_code((h2f((uint16_t)x[t]) - mn0) / s0);
+          const int c1 = clamp_code((h2f((uint16_t)(x[t] >> 16)) - mn1) / s1);
+          if (phys_ok(phys))
+            w.k_code[(((int64_t)phys * g.nkv + h) * P + t % P) * HDP + lane] =
+                (uint8_t)((c0 & 0x0f) | ((c1 & 0x0f) << 4));
+        }
+      }
+    }
+  } else {
+    // V: (token t, 32-channel group cg) per lane and pass
+    for (int it = lane; it < kGroup * HDG; it += 64) {
+      const int t = it / HDG, cg = it % HDG;
+      const uint16_t* row = xs + t * HD + cg * kGroup;
+      u32x4 v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = *(const u32x4*)(row + 8 * q);
+      float mn = h2f((uint16_t)v[0][0]), mx = mn;
+#pragma unroll
+      for (int k = 1; k < kGroup; ++k) {
+        const float x = h2f((uint16_t)(v[k / 8][(k % 8) / 2] >> (16 * (k & 1))));
+        mn = min_num(mn, x);
+        mx = max_num(mx, x);
+      }
+      float sv = (mx - mn) / 15.0f;
+      if (!(sv > 0.0f)) sv = 1.0f;
+      u32x4 codes;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int ch = 8 * q + k;
+          const float x = h2f((uint16_t)(v[ch / 8][(ch % 8) / 2] >> (16 * (ch & 1))));
+          word |= (uint32_t)clamp_code((x - mn) / sv) << (4 * k);
+        }
+        codes[q] = word;
+      }
+      const int phys = t < P ? p0 : p1;
+      if (table_ok && phys_ok(phys)) {
+        const int64_t tok = ((int64_t)phys * g.nkv + h) * P + t % P;
+        *(u32x4*)(w.v_code + tok * HDP + cg * (kGroup / 2)) = codes;
+        w.v_scale[tok * HDG + cg] = f2h(sv);
+        w.v_zero[tok * HDG + cg] = f2h(mn);
+      }
+    }
+  }
+  // shift: rows [0, R - 1) <- rows [32, R + 31) in forward chunks, every load
+  // of a chunk before its stores (a chunk's sources lie above every row it
+  // or an earlier chunk stores); the quantisation above read rows 0..31 first
+  constexpr int V16 = HD / 8;  // 16-byte pieces per row
+  const int units = (g.residual - 1) * V16;
+  constexpr int CH = 8;  // pieces per lane and chunk
+  for (int u0 = 0; u0 < units; u0 += 64 * CH) {
+    u32x4 buf[CH];
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int u = min(u0 + lane + 64 * k, units - 1);
+      buf[k] = *(const u32x4*)(xs + (int64_t)(u / V16 + kGroup) * HD + 8 * (u % V16));
+    }
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int u = u0 + lane + 64 * k;
+      if (u < units) *(u32x4*)(xs + (int64_t)(u / V16) * HD + 8 * (u % V16)) = buf[k];
+    }
+  }
+  // the new token: row R - 1 (live) and row r0 (the reference's stale copy)
+  if (lane < 2 * V16) {
+    const int row = lane < V16 ? g.residual - 1 : r0, piece = lane % V16;
+    *(u32x4*)(xs + (int64_t)row * HD + 8 * piece) = *(const u32x4*)(nx + 8 * piece);
+  }
+  // the stores above reach the point of coherence of every XCD before the flag
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  if (lane == 0)
+    __hip_atomic_store(a.ws_wflag + 2 * ((int64_t)b * g.nkv + h) + (is_v ? 1 : 0), a.epoch,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Writer wavefront wi of a.writer_waves: first the age-out items (sequence
+// rank among the aging ones, kv head, K | V) in turn, then the plain appends
+// of the other (sequence, kv head) pairs.
+template <int HD>
+__device__ __attribute__((always_inline)) inline void step_writer(const KiviGeo& g, const DecodeArgs& a, int wi,
+                                                                int lane) {
+  const int NW = a.writer_waves, NKV = g.nkv;
+  int rank0 = 0;  // aging sequences before this 64-sequence window
+  for (int base = 0; base < a.batch; base += 64) {
+    const int bb = base + lane;
+    const bool ag = bb < a.batch && step_ages(g, step_len(a, bb));
+    uint64_t m = __builtin_amdgcn_ballot_w64(ag);
+    int rank = rank0;
+    while (m) {
+      const int b = base + __builtin_ctzll(m);
+      m &= m - 1;
+      for (int k = 0; k < 2 * NKV; ++k) {
+        const int item = rank * 2 * NKV + k;
+        if (item % NW == wi) step_age_out<HD>(g, a, b, k >> 1, k & 1, lane);
+      }
+      ++rank;
+    }
+    rank0 = rank;
+  }
+  constexpr int V16 = HD / 8;
+  const AppendArgs& w = a.wr;
+  for (int p = wi; p < a.batch * NKV; p += NW) {
+    const int b = p / NKV, h = p - b * NKV;
+    const int L = step_len(a, b);
+    if (L < 1 || step_ages(g, L)) continue;
+    const int start = L - 1, r0 = start - split_old_tokens(start, g.residual);
+    if (r0 >= g.rs) continue;  // the writer's bound (in-scratch appends only)
+    if (lane < 2 * V16) {
+      const bool v = lane >= V16;
+      const int piece = lane % V16;
+      uint16_t* xs = (v ? w.v_scr : w.k_scr) + (int64_t)b * w.scr_stride + (int64_t)h * g.rs * HD;
+      const uint16_t* nx = (v ? w.new_v : w.new_k) + (int64_t)b * w.new_stride + (int64_t)h * HD;
+      *(u32x4*)(xs + (int64_t)r0 * HD + 8 * piece) = *(const u32x4*)(nx + 8 * piece);
+    }
+  }
+}
+
 // One run of the stream: units [x0, x1) of the concatenated (sequence, kv
 // head) streams, starting in sequence sp.b.  `first_seg` with first_* gives
 // the first segment's window when the caller has it already.  Partials of cut
 // segments go to slot b * NKV + h + w (w: the run's index), their flags after
 // the run.  Returns the s_memrealtime of the first group in LDS (profiling).
-template <int HD, int P, bool PACK>
+template <int HD, int P, bool PACK, bool FUSED>
 __device__ __attribute__((always_inline)) inline uint64_t stream_run(
     const KiviGeo& g, const DecodeArgs& a, StageBuf<HD>* ring, uint16_t* qrows, const Nibble& nb,
     float sscale, int lane, int64_t x0, int64_t x1, SeqSpan sp, bool first_seg, int first_T,
@@ -1263,6 +1488,42 @@ __device__ __attribute__((always_inline)) inline uint64_t stream_run(
     // previous wavefront owns: nothing here (no partial, no map entry)
     if (t_beg >= t_fin) continue;
 
+    // fused step: a segment whose sequence ages a group out reads its new
+    // group (tile g_age) and its residual rows only after the writer's two
+    // flags; in the others the residual row new_row (the new token) comes
+    // from NEW_K / NEW_V, never from the scratch the writer is storing to
+    int g_age = 0x7fffffff, new_row = -1;
+    bool ages = false, aging = false, waited = false;
+    if constexpr (FUSED) {
+      const int Lb = step_len(a, b);
+      ages = step_ages(g, Lb);
+      aging = ages && ov == split_old_tokens(Lb, g.residual);
+      if (aging)
+        g_age = ov / kGroup - 1;
+      else if (Lb == n && n > ov)
+        new_row = n - ov - 1;
+    }
+    auto wait_new = [&]() {
+      if (waited) return;
+      waited = true;
+      if (lane == 0) {
+        const uint64_t* f = a.ws_wflag + 2 * ((int64_t)b * NKV + h);
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        bool late = false;
+        while (ld_agent(f) != a.epoch || ld_agent(f + 1) != a.epoch) {
+          if (__builtin_amdgcn_s_memrealtime() - t0 > a.merge_timeout) {
+            late = true;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+        }
+        if (late && a.status)
+          __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
+      // the writer's stores (another XCD's L2 wrote them back) before any load
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    };
+
     // ---- quantised groups: a ring of S LDS stages, S - 1 in flight ----
     const int tq_end = min(t_fin, ov / kGroup);
     // read-only for the whole launch: the constant address space lets the
@@ -1276,6 +1537,9 @@ __device__ __attribute__((always_inline)) inline uint64_t stream_run(
     };
     uint32_t n0 = 0, n1 = 0;  // pages of group i + S - 1, read one group early
     if (t_beg < tq_end) {
+      if constexpr (FUSED) {
+        if (g_age >= t_beg && g_age < t_beg + S - 1 && g_age < tq_end) wait_new();
+      }
       wait_vm<0>();  // the counts below see only this segment's DMAs
 #pragma unroll
       for (int k = 0; k < S - 1; ++k)
@@ -1322,6 +1586,9 @@ __device__ __attribute__((always_inline)) inline uint64_t stream_run(
       for (int i = t_beg; i < tq_end; ++i) {
         const int ahead = slot == 0 ? S - 1 : slot - 1;  // (slot + S - 1) % S
         if (i + S - 1 < tq_end) {
+          if constexpr (FUSED) {
+            if (i + S - 1 == g_age) wait_new();
+          }
           load_stage<HD, P>(&ring[ahead], sb, n0, n1, lane);
           if (i + S < tq_end) {
             n0 = page(i + S, 0);
@@ -1346,8 +1613,11 @@ __device__ __attribute__((always_inline)) inline uint64_t stream_run(
     }
 
     // ---- fp16 residual tiles (all loads of a tile issued before its first use) ----
+    if constexpr (FUSED) {
+      if (aging && r_beg < t_fin) wait_new();
+    }
     for (int i = r_beg; i < t_fin; ++i) {
-      ResTile<HD> cur = load_res<HD>(a, g, b, h, ov, n, i, lane);
+      ResTile<HD> cur = load_res<HD, FUSED>(a, g, b, h, ov, n, i, lane, new_row);
       const int tn = min(kGroup, n - i * kGroup);  // 0 only for an empty sequence
       floatx4 sres[2];
 #pragma unroll
@@ -1480,6 +1750,15 @@ __device__ __attribute__((always_inline)) inline uint64_t stream_run(
       // only a run's first and last segments can be cut
       (t_beg == 0 ? cut_last : cut_first) = piece;
     }
+    // fused step: the wavefront that decoded the whole aging segment was its
+    // only reader; it clears the writer's flags (a cut one: its merge)
+    if constexpr (FUSED) {
+      if (ages && whole && lane == 0) {
+        uint64_t* f = a.ws_wflag + 2 * ((int64_t)b * NKV + h);
+        __hip_atomic_store(f, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(f + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
   // flags after the run: the partials are complete at the point of coherence
   // before their flags are
@@ -1499,7 +1778,7 @@ __device__ __attribute__((always_inline)) inline uint64_t stream_run(
 // loop, which at three waves per SIMD spills; they run with the register
 // budget of two (the v1 symbols decode one sequence, or the causal prefixes
 // of one, far from filling the device).
-template <int HD, int P, bool PACK, bool PQ>
+template <int HD, int P, bool PACK, bool PQ, bool FUSED>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     PQ ? 1 : min_waves_per_simd<HD, PACK>()))) void kivi_decode_stream_kernel(KiviGeo g,
                                                                               DecodeArgs a) {
@@ -1515,8 +1794,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
 
   const int lane = threadIdx.x;
   const uint64_t t_start = a.stamps ? __builtin_amdgcn_s_memrealtime() : 0;
-  if ((int)blockIdx.x >= a.waves) {
-    merge_segments<HD, PACK, PQ>(g, a, lane);
+  // fused step: writer wavefronts first, then the stream, then the merges
+  const int bid = (int)blockIdx.x - (FUSED ? a.writer_waves : 0);
+  if constexpr (FUSED) {
+    if (bid < 0) {
+      step_writer<HD>(g, a, (int)blockIdx.x, lane);
+      return;
+    }
+  }
+  if (bid >= a.waves) {
+    merge_segments<HD, PACK, PQ, FUSED>(g, a, lane);
     write_stamp(a, t_start, 0, lane);
     return;
   }
@@ -1531,14 +1818,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     for (int i = lane; i < (int)(sizeof(qrows) / 16); i += 64)
       ((u32x4*)qrows)[i] = u32x4{0u, 0u, 0u, 0u};
     const float sscale = 1.4426950408889634f / __builtin_sqrtf((float)HD);  // log2(e)/sqrt(HD)
-    for (int64_t r = blockIdx.x;; r += a.waves) {
+    for (int64_t r = bid;; r += a.waves) {
       const RunLoc rl = locate_run(g, a, r, lane);
       if (rl.q < 0) break;
       const int64_t TTq = (int64_t)g.nkv * rl.units, wl = r - rl.r0;
       const int64_t x0 = wl * TTq / rl.runs, x1 = (wl + 1) * TTq / rl.runs;
       if (x0 >= x1) continue;
-      stream_run<HD, P, PACK>(g, a, ring, qrows, nb, sscale, lane, x0, x1,
-                              SeqSpan{rl.q, 0, rl.units}, false, 0, 0, 0, (int)r);
+      stream_run<HD, P, PACK, false>(g, a, ring, qrows, nb, sscale, lane, x0, x1,
+                                     SeqSpan{rl.q, 0, rl.units}, false, 0, 0, 0, (int)r);
     }
     return;
   }
@@ -1556,7 +1843,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   const int64_t TT = one_pass ? (int64_t)NKV * __builtin_amdgcn_readlane(lane_incl, 63)
                               : stream_units(g, a, lane);
   const int64_t W = stream_waves(TT, a.waves);
-  const int w = blockIdx.x;
+  const int w = bid;
   if (w >= W) return;
   const int64_t x0 = (int64_t)w * TT / W, x1 = (int64_t)(w + 1) * TT / W;
   if (x0 >= x1) return;
@@ -1585,8 +1872,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   } else {
     sp = locate(g, a, x0, lane);
   }
-  const uint64_t t_first = stream_run<HD, P, PACK>(g, a, ring, qrows, nb, sscale, lane, x0, x1, sp,
-                                                   one_pass, first_T, first_ov, first_n, w);
+  const uint64_t t_first = stream_run<HD, P, PACK, FUSED>(
+      g, a, ring, qrows, nb, sscale, lane, x0, x1, sp, one_pass, first_T, first_ov, first_n, w);
   // profiling: the run's units (bits 0-31) and the ticks to its first group (32-63)
   write_stamp(a, t_start, (uint64_t)(x1 - x0) | ((t_first ? t_first - t_start : 0) << 32), lane);
 }
@@ -1594,19 +1881,28 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
 template <int HD, int P>
 static void launch_one(const KiviGeo& g, const DecodeArgs& a, hipStream_t stream,
                        hipEvent_t start, hipEvent_t stop) {
-  const dim3 grid(a.waves + a.merge_wgs);
-  if (g.gqa <= 8 && a.per_query)
-    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, true, true>), grid, dim3(64), 0,
+  const dim3 grid(a.writer_waves + a.waves + a.merge_wgs);
+  const dim3 block(64);
+  if (a.writer_waves > 0) {
+    if (g.gqa <= 8)
+      hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, true, false, true>), grid, block, 0,
+                            stream, start, stop, 0, g, a);
+    else
+      hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, false, false, true>), grid, block,
+                            0, stream, start, stop, 0, g, a);
+  } else if (g.gqa <= 8 && a.per_query) {
+    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, true, true, false>), grid, block, 0,
                           stream, start, stop, 0, g, a);
-  else if (g.gqa <= 8)
-    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, true, false>), grid, dim3(64), 0,
+  } else if (g.gqa <= 8) {
+    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, true, false, false>), grid, block, 0,
                           stream, start, stop, 0, g, a);
-  else if (a.per_query)
-    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, false, true>), grid, dim3(64), 0,
+  } else if (a.per_query) {
+    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, false, true, false>), grid, block, 0,
                           stream, start, stop, 0, g, a);
-  else
-    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, false, false>), grid, dim3(64), 0,
-                          stream, start, stop, 0, g, a);
+  } else {
+    hipExtLaunchKernelGGL((kivi_decode_stream_kernel<HD, P, false, false, false>), grid, block,
+                          0, stream, start, stop, 0, g, a);
+  }
 }
 
 hipError_t launch_decode_mfma(const KiviGeo& g, const DecodeArgs& args, int batch,
@@ -1662,7 +1958,7 @@ static int resident_per_cu() {
   static int n = 0;
   if (n == 0) {
     int k = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, kivi_decode_stream_kernel<HD, P, PACK, false>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, kivi_decode_stream_kernel<HD, P, PACK, false, false>,
                                                      64, 0) != hipSuccess ||
         k < 1)
       k = 8;

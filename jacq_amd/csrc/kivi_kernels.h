@@ -59,6 +59,13 @@ struct DecodeArgs {
   uint32_t* status = nullptr;  // matrix-core kernel: set to 1 when a merge wait runs out
   uint64_t* ws_poison = nullptr;  // matrix-core kernel: the workspace's poison word
   int per_query = 0;  // matrix-core kernel: cut each query's streams by its own length alone
+  // Fused write + decode (jacq_kivi_write_decode): the writer's arrays (one
+  // new token per sequence; its length before the write is seq_lens - 1), the
+  // writer wavefronts at the front of the grid, and per (sequence, kv head,
+  // K | V) the epoch of the launch whose writer finished that age-out.
+  AppendArgs wr{};
+  uint64_t* ws_wflag = nullptr;
+  int writer_waves = 0;
 };
 
 // Decode window of one sequence.  Dense: the split rule (decode_window).

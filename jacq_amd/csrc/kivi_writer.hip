@@ -27,42 +27,11 @@ typedef uint32_t w2 __attribute__((ext_vector_type(2)));
 
 #pragma clang fp contract(off)
 
-// static_cast<int>(rintf(x)) clamped to [0, 15] (source_patch.py:1517-1522),
-// with the conversion CUDA and gfx950 hardware perform: out-of-range values
-// saturate, NaN becomes 0.  Clamped in the float domain, because an
-// out-of-range float -> int conversion is undefined in C++ and the compiler
-// may assume it does not happen.
-__device__ inline int clamp_code(float x) {
-  const float r = __builtin_rintf(x);
-  if (r >= 15.0f) return 15;
-  if (r >= 0.0f) return (int)r;
-  return 0;  // negative or NaN
-}
-
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
 // operations, not for its global stores (those have no reader in the kernel).
 // The memory clobber keeps the compiler from moving LDS accesses across it.
 __device__ inline void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// fminf / fmaxf of the reference's age-out kernels (source_patch.py:1555-1558,
-// :1598-1599): a NaN operand is dropped, NaN results only when both are NaN.
-// For a +0 / -0 pair, min gives -0 and max +0 (C Annex F's recommendation;
-// LLVM's minnum leaves it open, so it is written out).  Both are then
-// commutative and associative: the partial reductions below may merge in any
-// order and still give one sequential loop's bits.
-__device__ inline float min_num(float a, float b) {
-  if (b != b) return a;
-  if (a != a) return b;
-  if (a == b) return __uint_as_float(__float_as_uint(a) | __float_as_uint(b));
-  return b < a ? b : a;
-}
-__device__ inline float max_num(float a, float b) {
-  if (b != b) return a;
-  if (a != a) return b;
-  if (a == b) return __uint_as_float(__float_as_uint(a) & __float_as_uint(b));
-  return b > a ? b : a;
 }
 
 __global__ __launch_bounds__(kWriterThreads) __attribute__((amdgpu_waves_per_eu(2))) void kivi_append_kernel(KiviGeo g, AppendArgs a) {

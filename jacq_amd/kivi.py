@@ -148,6 +148,11 @@ def lib() -> ctypes.CDLL:
     L.jacq_kivi_init.restype = ctypes.c_int
     L.jacq_kivi_decode_status.argtypes = [_vp, ctypes.c_size_t, _vp]
     L.jacq_kivi_decode_status.restype = ctypes.c_int
+    L.jacq_kivi_write_decode.argtypes = [ctypes.POINTER(Geometry)] + [_vp] * 13 + [
+        _i32, _vp, _vp, ctypes.c_size_t, _vp]
+    L.jacq_kivi_write_decode.restype = ctypes.c_int
+    L.jacq_kivi_write_decode_workspace_size.argtypes = [ctypes.POINTER(Geometry), _i32]
+    L.jacq_kivi_write_decode_workspace_size.restype = ctypes.c_size_t
     L.jacq_kivi_release_workspaces.argtypes = []
     L.jacq_kivi_release_workspaces.restype = ctypes.c_int
     L.jacq_kivi_test_device_allocations.argtypes = []
@@ -629,6 +634,37 @@ class PagedKiviCache:
         rc = lib().jacq_kivi_decode(ctypes.byref(geo), _ptr(q), _ptr(seq_lens), _ptr(block_tables),
                                     *[_ptr(t) for t in self.pool()], self.batch, _ptr(out),
                                     _ptr(workspace), ws_bytes, _stream(q.device))
+        if rc != 0:
+            _raise(rc)
+        return out
+
+    def write_decode(self, q: torch.Tensor, new_k: torch.Tensor, new_v: torch.Tensor,
+                     seq_lens: torch.Tensor, block_tables: torch.Tensor,
+                     out: torch.Tensor | None = None, workspace: torch.Tensor | None = None
+                     ) -> torch.Tensor:
+        """One fused step (jacq_kivi_write_decode): append new_k/new_v
+        [batch, NKV, HD] fp16 at position seq_lens - 1, then decode q
+        [batch, NH, HD] over the new state -> O [batch, NH, HD] fp32."""
+        g = self.geo
+        check_shape(q, (self.batch, g.num_heads, g.head_dim), "Q")
+        _check(q.dtype == torch.float16 and q.is_contiguous(), "Q must be contiguous fp16")
+        for t, name in ((new_k, "NEW_K"), (new_v, "NEW_V")):
+            check_shape(t, (self.batch, g.num_kv_heads, g.head_dim), name)
+            _check(t.dtype == torch.float16 and t.is_contiguous(), name + " must be contiguous fp16")
+        check_shape(seq_lens, (self.batch,), "SEQ_LENS")
+        _check(seq_lens.dtype == torch.int32, "SEQ_LENS must be int32")
+        check_shape(block_tables, (self.batch, g.max_pages_per_seq), "BLOCK_TABLES")
+        _check(block_tables.dtype == torch.int32 and block_tables.is_contiguous(),
+               "BLOCK_TABLES must be contiguous int32")
+        if out is None:
+            out = torch.empty((self.batch, g.num_heads, g.head_dim), dtype=torch.float32,
+                              device=q.device)
+        geo = g.c()
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        rc = lib().jacq_kivi_write_decode(ctypes.byref(geo), _ptr(q), _ptr(new_k), _ptr(new_v),
+                                          _ptr(seq_lens), _ptr(block_tables),
+                                          *[_ptr(t) for t in self.pool()], self.batch, _ptr(out),
+                                          _ptr(workspace), ws_bytes, _stream(q.device))
         if rc != 0:
             _raise(rc)
         return out

@@ -1,8 +1,9 @@
 """Parity at the benchmark's full sizes.
 
 * qwen14b (the headline config: 64 sequences, contexts U[1024,16384], page 16):
-  the HIP writer builds every sequence from its history, then one fused step
-  writes a token to every sequence; the whole pool and the live scratch rows
+  the HIP writer builds every sequence from its history, then one step
+  writes a token to every sequence and decodes (a writer launch then a decode
+  launch, or one jacq_kivi_write_decode launch); the whole pool and the live scratch rows
   must equal the oracle's bit for bit, and the decode of the whole batch must
   be within max-abs 2e-3 / rel 1e-2 of the oracle's fp32 online decode.
 * long (256 sequences, contexts U[4096,32768], K with 1% +-20 spikes): the
@@ -73,7 +74,10 @@ def _geometry(kivi, w, max_pages, num_pages):
     return kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, max_pages, num_pages)
 
 
-def test_fullsize_qwen14b_writer_and_decode(kivi):
+@pytest.mark.parametrize("fused", [False, True], ids=["append_then_decode", "write_decode"])
+def test_fullsize_qwen14b_writer_and_decode(kivi, fused):
+    """The last token of every sequence goes in by one step: the writer
+    launch then the decode launch, or the fused jacq_kivi_write_decode."""
     w = wl.WORKLOADS["qwen14b"]
     rng = np.random.default_rng(w.seed)
     lens = wl.context_lens(w, rng)
@@ -91,14 +95,22 @@ def test_fullsize_qwen14b_writer_and_decode(kivi):
         cache.sequence_view(b).append(k[None, :-1].contiguous(), v[None, :-1].contiguous(),
                                       bt[b:b + 1].contiguous(), zero)
         hist.append((k, v))
-    # one fused step: a token for every sequence
-    nk = torch.stack([k[-1] for k, _ in hist])[:, None].contiguous()
-    nv = torch.stack([v[-1] for _, v in hist])[:, None].contiguous()
-    cache.append(nk, nv, bt, torch.from_numpy(lens.astype(np.int32)).to(dev))
+    # one step: a token for every sequence
+    nk = torch.stack([k[-1] for k, _ in hist]).contiguous()
+    nv = torch.stack([v[-1] for _, v in hist]).contiguous()
     final = lens + 1
     q = torch.randn((w.batch, w.nh, w.hd), generator=gen, device=dev).half()
-    out = cache.decode(q, torch.from_numpy(final.astype(np.int32)).to(dev), bt)
+    after = torch.from_numpy(final.astype(np.int32)).to(dev)
+    if fused:
+        out = cache.write_decode(q, nk, nv, after, bt)
+    else:
+        cache.append(nk[:, None].contiguous(), nv[:, None].contiguous(), bt,
+                     torch.from_numpy(lens.astype(np.int32)).to(dev))
+        out = cache.decode(q, after, bt)
     torch.cuda.synchronize()
+    ages = sum(wl.split_old_tokens(int(n) + 1, w.residual) > wl.split_old_tokens(int(n), w.residual)
+               for n in lens)
+    print(f"qwen14b step: {ages} of {w.batch} sequences age a group out", flush=True)
 
     geo = o.Geometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, max_pages)
     ref = o.Cache.empty(geo, num_pages, w.batch)
@@ -115,7 +127,7 @@ def test_fullsize_qwen14b_writer_and_decode(kivi):
             r = int(final[b] - wl.split_old_tokens(int(final[b]), w.residual))
             assert np.array_equal(got[b, :, :r], want[b, :, :r]), f"{name}[{b}] differs"
     want = o.decode_batch(ref, _u16(q), final.astype(np.int32), tables, nthreads=THREADS)
-    assert_close(out.cpu().numpy(), want, "qwen14b full-size decode")
+    assert_close(out.cpu().numpy(), want, f"qwen14b full-size decode (fused={fused})")
 
 
 def test_fullsize_long_recipe_sampled_parity_and_permutation(kivi):

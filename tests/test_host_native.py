@@ -78,7 +78,8 @@ def test_header_declares_the_reference_symbols():
         "jacq_kivi_plan_batched_write", "jacq_kivi_profile_start", "jacq_kivi_profile_stop",
         "jacq_kivi_profile_write_ms", "jacq_kivi_profile_wave_stamps", "jacq_kivi_init",
         "jacq_kivi_decode_status", "jacq_kivi_release_workspaces",
-        "jacq_kivi_test_device_allocations",
+        "jacq_kivi_test_device_allocations", "jacq_kivi_write_decode",
+        "jacq_kivi_write_decode_workspace_size",
         "jacq_kivi_test_force_merge_timeout", "jacq_kivi_decode_noalloc"])
 
 
