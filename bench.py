@@ -2,31 +2,34 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload qwen14b]
 
-A step is one pass of the hot path over the batch: the cache writer appends
-one new token to every sequence (aging out 32-token groups where a sequence
-crosses the residual window), then paged decode attention runs for one query
-token per sequence.  Inputs are synthetic (seeded N(0,1) with outlier K
+A step is one pass of the hot path over the batch, in one launch
+(jacq_kivi_write_decode): the cache writer appends one new token to every
+sequence (aging out 32-token groups where a sequence crosses the residual
+window), then paged decode attention runs for one query token per sequence
+over the new state.  Inputs are synthetic (seeded N(0,1) with outlier K
 channels, BASELINE workload definitions in jacq_amd/workloads.py) and resident
-in HBM before timing starts.  Each step is bracketed by HIP events on the
-stream the kernels run on; a 512 MiB buffer is read (by default) before every step so
-the 256 MiB MALL and the L2 start cold.
+in HBM before timing starts.  A 512 MiB buffer is read (by default) before
+every step so the 256 MiB MALL and the L2 start cold.
 
-Prints ONE JSON line.  `value` is the effective KV bandwidth of the decode
-(algorithmic bytes / decode time, GB/s); the decode time is the GPU time of
-the decode launch (one kernel: the stream wavefronts, then the workgroups
-that merge the split-K partials) from HIP events the library records on the
-launch stream before and after it (jacq_kivi_profile_*), and `ms_per_step` is
-that time per step.  `roofline.achieved` is the same bytes over the same
-event-timed decode.  A second pass of the same number of steps, continuing the
-token stream, launches the kernel with start / stop events that the command
-processor stamps at the kernel's own start and end: `kernel_us` and
+Prints ONE JSON line.  `value` is the effective KV bandwidth of the step
+(the decode's algorithmic bytes / step time, GB/s; the writer's few MB are not
+counted); the step time is the GPU time of the fused launch (one kernel: the
+writer wavefronts, the decode's stream wavefronts, then the workgroups that
+merge the split-K partials) from HIP events the library records on the launch
+stream before and after it (jacq_kivi_profile_*), and `ms_per_step` is that
+time per step.  `roofline.achieved` is the same bytes over the same time.
+A second pass of the same number of steps, continuing the token stream,
+launches the kernel with start / stop events that the command processor
+stamps at the kernel's own start and end: `kernel_us` and
 `roofline.kernel_stamped_frac` come from it (that launch form delays the next
-kernel by a few microseconds, so the timed pass leaves it out).  Before the
-warmup and before the timed steps a GPU spin of --lead-ms is enqueued, so the
-host enqueues every step ahead of the GPU and the GPU never idles between
-steps waiting for Python (without it the first pass's kernels ran about 4 us
-slower than the second's).  `host_bracketed_us` adds the host-side gaps (Python argument checks
-before each launch) seen by events recorded around the Python calls.  The CPU
+kernel by a few microseconds, so the timed pass leaves it out).  A third pass
+runs the same steps as two launches, the writer then the plain decode
+(`two_launch_step`).  Before each pass's warmup and before its timed steps a
+GPU spin of --lead-ms is enqueued, so the host enqueues every step ahead of
+the GPU and the GPU never idles between steps waiting for Python (without it
+the first pass's kernels ran about 4 us slower than the second's).
+`host_bracketed_us` adds the host-side gaps (Python argument checks before
+each launch) seen by events recorded around the Python calls.  The CPU
 baseline runs the oracle (oracle/, a C restatement of the reference path) over
 the same state on this host's cores.
 """
@@ -96,8 +99,8 @@ def main() -> int:
     rng = np.random.default_rng(w.seed)
     lens0 = wl.context_lens(w, rng)            # lengths when timing starts (after prefill)
     total_steps = args.warmup + args.steps
-    # two passes of warmup + steps each (below): room for all their tokens
-    tables_np, num_pages, max_pages = wl.block_tables(w, lens0 + 2 * total_steps + 1, rng)
+    # three passes of warmup + steps each (below): room for all their tokens
+    tables_np, num_pages, max_pages = wl.block_tables(w, lens0 + 3 * total_steps + 1, rng)
     outl = wl.outlier_channels(w, rng)
     B = w.batch
     geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, w.group, w.residual, max_pages, num_pages)
@@ -134,15 +137,16 @@ def main() -> int:
         f"pages={num_pages}")
 
     # ---- per-step inputs ----
-    qs = torch.randn((2 * total_steps, B, w.nh, w.hd), generator=gen, device=dev).half()
-    nk = torch.randn((2 * total_steps, B, 1, w.nkv, w.hd), generator=gen, device=dev).half()
-    nv = torch.randn((2 * total_steps, B, 1, w.nkv, w.hd), generator=gen, device=dev).half()
+    qs = torch.randn((3 * total_steps, B, w.nh, w.hd), generator=gen, device=dev).half()
+    nk = torch.randn((3 * total_steps, B, w.nkv, w.hd), generator=gen, device=dev).half()
+    nv = torch.randn((3 * total_steps, B, w.nkv, w.hd), generator=gen, device=dev).half()
     out = torch.empty((B, w.nh, w.hd), dtype=torch.float32, device=dev)
     lens_before = torch.from_numpy(lens0.astype(np.int32)).to(dev)
     lens_after = lens_before + 1
     flush = None if args.no_flush else torch.ones(512 << 20, dtype=torch.uint8, device=dev)
     flush_sink = torch.zeros(1, dtype=torch.int64, device=dev)
-    ws_bytes = kivi.lib().jacq_kivi_decode_workspace_size(ctypes_geo(kivi, geo), B)
+    ws_bytes = max(kivi.lib().jacq_kivi_decode_workspace_size(ctypes_geo(kivi, geo), B),
+                   kivi.lib().jacq_kivi_write_decode_workspace_size(ctypes_geo(kivi, geo), B))
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
 
     stream = torch.cuda.current_stream(dev)
@@ -166,11 +170,13 @@ def main() -> int:
         if spin_cycles:
             torch.cuda._sleep(spin_cycles)
 
-    def timed_pass(step0: int, split: bool):
-        """warmup + steps of (flush, append, decode) from global step step0;
-        the library's events bracket the decode launch (split: stamped by the
-        command processor at the kernel's own start and end).  Returns
-        per-step arrays of the timed steps and the wall time."""
+    def timed_pass(step0: int, split: bool, fused: bool):
+        """warmup + steps from global step step0, each a cache flush then one
+        step of the hot path: the fused write + decode launch, or (not fused)
+        the writer launch then the decode launch.  The library's events
+        bracket the decode launch -- the fused one or the plain decode (split:
+        stamped by the command processor at the kernel's own start and end).
+        Returns per-step arrays of the timed steps and the wall time."""
         evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)]
                for _ in range(total_steps)]
         torch.cuda.synchronize()
@@ -193,12 +199,17 @@ def main() -> int:
                     flush.fill_(gi & 0xff)
             e = evs[i]
             e[0].record(stream)
-            cache.append(nk[gi], nv[gi], bt, lens_before)
+            if not fused:
+                cache.append(nk[gi][:, None], nv[gi][:, None], bt, lens_before)
             e[1].record(stream)
-            if stamps is not None and not split and i >= args.warmup:
+            if stamps is not None and not split and fused and i >= args.warmup:
                 kivi.lib().jacq_kivi_profile_wave_stamps(
                     kivi._ptr(stamps[i - args.warmup]), STAMP_CAP)
-            cache.decode(qs[gi], lens_after, bt, out=out, workspace=workspace)
+            if fused:
+                cache.write_decode(qs[gi], nk[gi], nv[gi], lens_after, bt, out=out,
+                                   workspace=workspace)
+            else:
+                cache.decode(qs[gi], lens_after, bt, out=out, workspace=workspace)
             if stamps is not None:
                 kivi.lib().jacq_kivi_profile_wave_stamps(None, 0)
             e[2].record(stream)
@@ -211,40 +222,44 @@ def main() -> int:
         host = [(evs[i][0].elapsed_time(evs[i][1]), evs[i][1].elapsed_time(evs[i][2]))
                 for i in range(args.warmup, total_steps)]
         return (np.array(kern_ms[args.warmup:]), np.array(merge_ms[args.warmup:]),
-                np.array(write_ms[args.warmup:]), np.array(host), wall)
+                np.array(write_ms[args.warmup:]) if not fused else None, np.array(host), wall)
 
-    # pass 1 (the timed region of the contract): events only around each
-    # decode, so the figure is the decode exactly as a caller runs it
+    # pass 1 (the timed region of the contract): the fused step, events only
+    # around each launch, so the figure is the step exactly as a caller runs it
+    # pass 2: the same steps continued, the fused kernel's own start and end
+    # stamped by the command processor (kernel_us, roofline cross-check)
+    # pass 3: the same steps as two launches (writer, then decode), for the
+    # comparison
+    p1, p2, p3 = 0, total_steps, 2 * total_steps
     if args.swap_passes:
-        kern, _, _, _, _ = timed_pass(0, split=True)
-        dec, _, wgpu, host, wall = timed_pass(total_steps, split=False)
+        p1, p2 = p2, p1
+        kern, _, _, _, _ = timed_pass(p2, split=True, fused=True)
+        dec, _, _, host, wall = timed_pass(p1, split=False, fused=True)
     else:
-        dec, _, wgpu, host, wall = timed_pass(0, split=False)
+        dec, _, _, host, wall = timed_pass(p1, split=False, fused=True)
         if stamps is not None:
             np.save(args.wave_stamps, stamps.cpu().numpy())
-        # pass 2: the same steps continued, the kernel's own start and end
-        # stamped by the command processor (roofline)
-        kern, _, _, _, _ = timed_pass(total_steps, split=True)
+        kern, _, _, _, _ = timed_pass(p2, split=True, fused=True)
+    sep_dec, _, sep_wr, _, _ = timed_pass(p3, split=False, fused=False)
 
     def bytes_of(step0):
         return [geometry.decode_step_bytes(lens0 + step0 + i + 1, w.nh, w.nkv, w.hd, w.page,
                                          w.residual, w.group)
                 for i in range(args.warmup, total_steps)]
-    dec0, kern0 = (total_steps, 0) if args.swap_passes else (0, total_steps)
-    step_bytes = bytes_of(dec0)
-    # GPU time of the decode launch from the events the library records on
-    # the launch stream; host-side gaps before a launch
-    # (Python argument checks) are excluded, host_bracketed_* keep them
-    wr = wgpu
-    host_wr, host_dec = host[:, 0], host[:, 1]
+    step_bytes = bytes_of(p1)
+    # GPU time of the launch from the events the library records on the launch
+    # stream; host-side gaps before a launch (Python argument checks) are
+    # excluded, host_bracketed_* keep them
+    host_dec = host[:, 1]
     gbs = float(np.sum(step_bytes) / (dec.sum() * 1e-3) / 1e9)
-    kern_gbs = float(np.sum(bytes_of(kern0)) / (kern.sum() * 1e-3) / 1e9)
+    kern_gbs = float(np.sum(bytes_of(p2)) / (kern.sum() * 1e-3) / 1e9)
+    sep_gbs = float(np.sum(bytes_of(p3)) / (sep_dec.sum() * 1e-3) / 1e9)
     bytes_per_step = float(np.mean(step_bytes))
 
     # ---- CPU baseline: the oracle over the same final state on this host ----
     cpu = None
     if not args.no_cpu_baseline:
-        last = 2 * total_steps  # the state after the last decode of pass 2
+        last = 3 * total_steps  # the state after the last decode of pass 3
         cpu = cpu_baseline(args, w, cache, qs[last - 1], lens0 + last, tables_np,
                            out, max_pages,
                            bytes_per_step_last=geometry.decode_step_bytes(
@@ -267,37 +282,41 @@ def main() -> int:
         "config": {
             "workload": f"{w.name}: {w.nh}q/{w.nkv}kv heads, head_dim {w.hd}, batch {B}, "
                         f"context U[{w.ctx_lo},{w.ctx_hi}], page {w.page}, group {w.group}, "
-                        f"residual {w.residual}, int4 KIVI K/V, per step one cache write "
-                        f"launch then one decode launch (not fused)",
+                        f"residual {w.residual}, int4 KIVI K/V, per step one fused launch "
+                        f"(jacq_kivi_write_decode): append one token per sequence, aging "
+                        f"32-token groups out where a sequence crosses the residual window, "
+                        f"then decode one query per sequence",
             "batch": B,
             "mean_context": float(np.mean(lens0)),
             "pages": num_pages,
             "cold_cache": flush is not None,
             "cache_flush": None if flush is None else f"{args.flush} 512 MiB before each step",
         },
-        "decode_us": {"mean": round(float(dec.mean()) * 1e3, 2),
-                      "min": round(float(dec.min()) * 1e3, 2),
-                      "median": round(float(np.median(dec)) * 1e3, 2),
-                      "p90": round(float(np.percentile(dec, 90)) * 1e3, 2)},
+        "step_us": {"mean": round(float(dec.mean()) * 1e3, 2),
+                    "min": round(float(dec.min()) * 1e3, 2),
+                    "median": round(float(np.median(dec)) * 1e3, 2),
+                    "p90": round(float(np.percentile(dec, 90)) * 1e3, 2)},
         "kernel_us": {"mean": round(float(kern.mean()) * 1e3, 2),
                       "median": round(float(np.median(kern)) * 1e3, 2),
                       "min": round(float(kern.min()) * 1e3, 2)},
-        "write_us": {"mean": round(float(wr.mean()) * 1e3, 2),
-                     "median": round(float(np.median(wr)) * 1e3, 2)},
-        "host_bracketed_us": {"decode": round(float(host_dec.mean()) * 1e3, 2),
-                              "write": round(float(host_wr.mean()) * 1e3, 2)},
-        "step_us_write_plus_decode": round(float((dec + wr).mean()) * 1e3, 2),
+        "host_bracketed_us": round(float(host_dec.mean()) * 1e3, 2),
+        "two_launch_step": {
+            "write_us": round(float(sep_wr.mean()) * 1e3, 2),
+            "decode_us": round(float(sep_dec.mean()) * 1e3, 2),
+            "write_plus_decode_us": round(float((sep_wr + sep_dec).mean()) * 1e3, 2),
+            "decode_only_frac": round(sep_gbs / HBM_PEAK_GBS, 4),
+        },
         "decode_bytes_per_step": int(bytes_per_step),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "wall_s_timed_region": round(wall, 4),
         "roofline": {
-            "kernel": "kivi_decode_stream_kernel",
+            "kernel": "kivi_decode_stream_kernel<128, 16, true, false, true> (fused write + decode)",
             "bound": "hbm",
             "achieved": round(gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "timing": "HIP events on the launch stream around each decode of the timed pass",
+            "timing": "HIP events on the launch stream around each fused launch of the timed pass",
             "kernel_stamped_frac": round(kern_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
         },

@@ -347,13 +347,15 @@ void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& 
 }
 
 // Fused write + decode: writer wavefronts at the front of the grid (about one
-// per 16 (sequence, kv head, K | V) items, at most 64), and one epoch flag per
-// item after the split-K workspace.
+// per 16 (sequence, kv head, K | V) pairs, at most 64), and one epoch flag per
+// age-out item (sequence, kv head, K | V, 32-channel slice) after the split-K
+// workspace.
 int step_writer_waves(const KiviGeo& g, int batch) {
-  return std::max(1, std::min(64, 2 * batch * g.nkv / 16));
+  return std::max(1, std::min(128, 2 * batch * g.nkv / 8));
 }
 size_t step_flag_bytes(const KiviGeo& g, int batch) {
-  return (size_t)2 * batch * g.nkv * sizeof(uint64_t);
+  // K and V, one per 32-channel slice each
+  return (size_t)2 * (g.hd / jacq::kGroup) * batch * g.nkv * sizeof(uint64_t);
 }
 
 // ---- measurement hook: HIP events around the decode ----

@@ -257,11 +257,19 @@ __device__ inline uint32_t lds_addr(const void* p) {
 // read M0 in the instruction right after the SALU write of it (the GFX9
 // M0 / LDS-DMA hazard: one wait state); the compiler's hazard recognizer does
 // not look inside asm, so the s_nop is written here.
-template <int SZ, int OFF>
+// COH: device-scope load (sc1) instead of the non-temporal hint -- for data
+// another wavefront of the same launch stored with device-scope stores (the
+// fused step's age-outs), which a non-temporal load could find stale in this
+// XCD's L2.
+template <int SZ, int OFF, bool COH = false>
 __device__ inline void dma(uint64_t addr, uint32_t dst) {
   static_assert(OFF >= 0 && OFF < 4096, "global immediate offset range");
   const uint32_t m0 = dst - OFF;
-  if constexpr (SZ == 16)
+  if constexpr (COH) {
+    static_assert(SZ == 16, "device-scope LDS DMA: 16 bytes per lane");
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off offset:%2 sc1"
+                 :: "s"(m0), "v"(addr), "n"(OFF) : "memory", "m0");
+  } else if constexpr (SZ == 16)
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off offset:%2 nt"
                  :: "s"(m0), "v"(addr), "n"(OFF) : "memory", "m0");
   else if constexpr (SZ == 4)
@@ -273,12 +281,16 @@ __device__ inline void dma(uint64_t addr, uint32_t dst) {
 }
 
 // The same with a wave-uniform 64-bit base in SGPRs and a 32-bit lane offset.
-template <int OFF>
+template <int OFF, bool COH = false>
 __device__ inline void dma16s(uint64_t sbase, uint32_t voff, uint32_t dst) {
   static_assert(OFF >= 0 && OFF < 4096, "global immediate offset range");
   const uint32_t m0 = dst - OFF;
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:%3 nt"
-               :: "s"(m0), "v"(voff), "s"(sbase), "n"(OFF) : "memory", "m0");
+  if constexpr (COH)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:%3 sc1"
+                 :: "s"(m0), "v"(voff), "s"(sbase), "n"(OFF) : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:%3 nt"
+                 :: "s"(m0), "v"(voff), "s"(sbase), "n"(OFF) : "memory", "m0");
 }
 
 template <int N>
@@ -331,7 +343,7 @@ constexpr int min_waves_per_simd() {
 
 // Issue the DMAs of one group whose tokens 0..P-1 sit in page p0 and the
 // rest (page size 16) in p1.
-template <int HD, int P>
+template <int HD, int P, bool COH = false>
 __device__ inline void load_stage(StageBuf<HD>* buf, const StageBases& sb, uint32_t p0,
                                   uint32_t p1, int lane) {
   const uint32_t base = lds_addr(buf);
@@ -342,23 +354,23 @@ __device__ inline void load_stage(StageBuf<HD>* buf, const StageBases& sb, uint3
     // 1 KiB = 16 token rows per DMA: rows 0-15 and 16-31
     const uint64_t o0 = (uint64_t)p0 * sb.code_page;
     const uint64_t o1 = P == 16 ? (uint64_t)p1 * sb.code_page : o0 + 1024;
-    dma16s<0>(sb.kc + o0, lo, kd);
-    dma16s<0>(sb.kc + o1, lo, kd + 1024);
-    dma16s<0>(sb.vc + o0, lo, vd);
-    dma16s<0>(sb.vc + o1, lo, vd + 1024);
+    dma16s<0, COH>(sb.kc + o0, lo, kd);
+    dma16s<0, COH>(sb.kc + o1, lo, kd + 1024);
+    dma16s<0, COH>(sb.vc + o0, lo, vd);
+    dma16s<0, COH>(sb.vc + o1, lo, vd + 1024);
   } else if constexpr (P == 32) {
     const uint64_t o0 = (uint64_t)p0 * sb.code_page;
-    dma16s<0>(sb.kc + o0, lo, kd);
-    dma16s<0>(sb.vc + o0, lo, vd);
+    dma16s<0, COH>(sb.kc + o0, lo, kd);
+    dma16s<0, COH>(sb.vc + o0, lo, vd);
   } else {
     // one DMA spans both pages: lanes 0-31 rows 0-15 of p0, lanes 32-63 of p1
     const uint64_t o = (uint64_t)(lane < 32 ? p0 : p1) * sb.code_page + (lo & 511u);
-    dma<16, 0>(sb.kc + o, kd);
-    dma<16, 0>(sb.vc + o, vd);
+    dma<16, 0, COH>(sb.kc + o, kd);
+    dma<16, 0, COH>(sb.vc + o, vd);
   }
   const uint32_t sd = base + (uint32_t)offsetof(StageBuf<HD>, s);
   const uint64_t sa = sb.sc + (uint64_t)(sb.sc_p1 ? p1 : p0) * sb.sc_page;
-  if (sb.sc_on) dma<16, 0>(sa, sd);
+  if (sb.sc_on) dma<16, 0, COH>(sa, sd);
 }
 
 // IEEE maximum (llvm.maximum): lowers to v_maximum3_f32 without the
@@ -849,7 +861,23 @@ struct ResTile {
 
 // FUSED: residual row new_row (>= 0) is the step's new token, read from
 // NEW_K / NEW_V.
-template <int HD, bool FUSED>
+// Rows of a residual tile: non-temporal loads, or (COH) device-scope loads
+// of eight bytes at a time, for rows the fused step's writer just shifted.
+template <typename V, bool COH>
+__device__ inline V ld_rows(const uint16_t* p) {
+  if constexpr (COH) {
+    constexpr int N = sizeof(V) / 8;
+    uint64_t w[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      w[i] = __hip_atomic_load((const uint64_t*)p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __builtin_bit_cast(V, w);
+  } else {
+    return __builtin_nontemporal_load((const V*)p);
+  }
+}
+
+template <int HD, bool FUSED, bool COH>
 __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, int b, int h,
                                        int ov, int n, int tile, int lane, int new_row) {
   constexpr int KS = HD / 32, CPL = HD / 16;
@@ -882,13 +910,12 @@ __device__ inline ResTile<HD> load_res(const DecodeArgs& a, const KiviGeo& g, in
     const uint16_t* kr = krow(r0 + (tl < tn ? tl : 0)) + j * (HD / 4);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      rt.kv[tt][ks] = __builtin_nontemporal_load((const u32x4*)(kr + 8 * ks));
+      rt.kv[tt][ks] = ld_rows<u32x4, COH>(kr + 8 * ks);
   }
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
     const int tl = 8 * j + r;
-    rt.vr[r] = __builtin_nontemporal_load(
-        (const typename ResTile<HD>::vrow_t*)(vrow(r0 + (tl < tn ? tl : 0)) + CPL * c));
+    rt.vr[r] = ld_rows<typename ResTile<HD>::vrow_t, COH>(vrow(r0 + (tl < tn ? tl : 0)) + CPL * c);
   }
   return rt;
 }
@@ -1033,6 +1060,12 @@ __device__ inline floatx4 ld_agent4(const float* p) {
   return v;
 }
 __device__ inline void keep(floatx4& v) { asm volatile("" : "+v"(v)); }
+// Device-scope (sc1) store of one to eight bytes: the fused step's writer
+// stores what decode wavefronts of the same launch, on any XCD, read next.
+template <typename T>
+__device__ inline void st_dev(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ inline float lo_f(uint64_t v) { return __uint_as_float((uint32_t)v); }
 __device__ inline float hi_f(uint64_t v) { return __uint_as_float((uint32_t)(v >> 32)); }
 
@@ -1218,11 +1251,9 @@ __device__ __attribute__((always_inline)) inline void merge_segments(const KiviG
     // fused step: every piece of the segment has landed, so its readers of
     // the writer's age-out are done; its flags start the next launch at zero
     if constexpr (FUSED) {
-      if (lane == 0 && step_ages(g, step_len(a, b))) {
-        uint64_t* f = a.ws_wflag + 2 * (int64_t)seg;
-        __hip_atomic_store(f, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(f + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      if (lane < 2 * (HD / kGroup) && step_ages(g, step_len(a, b)))
+        __hip_atomic_store(a.ws_wflag + 2 * (HD / kGroup) * (int64_t)seg + lane, 0ull,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   // a wait ran out (or an earlier one poisoned the workspace): the workspace
@@ -1254,17 +1285,32 @@ __device__ __attribute__((always_inline)) inline void merge_segments(const KiviG
 // The arithmetic is the writer kernel's (kivi_append_kernel), so pages and
 // scratch end bit for bit as a separate write would leave them.
 
+// Flags per (sequence, kv head): K and V, one per 32-channel slice each.
 template <int HD>
-__device__ __attribute__((always_inline)) inline void step_age_out(const KiviGeo& g, const DecodeArgs& a,
-                                                        int b, int h, bool is_v, int lane) {
+constexpr int step_flags() {
+  return 2 * (HD / kGroup);
+}
+
+// One age-out item: channels [32 q, 32 q + 32) of K or V of (sequence b, kv
+// head h).  The slice is self-contained: K is quantised per channel (over the
+// group's 32 tokens) and V per (token, 32-channel group), so the slice's codes
+// and scales need only its own rows, and the slice's shift touches no other
+// item's bytes -- items need no ordering among themselves.
+template <int HD>
+__device__ __attribute__((always_inline)) inline void step_age_out(const KiviGeo& g,
+                                                                   const DecodeArgs& a, int b,
+                                                                   int h, bool is_v, int q,
+                                                                   int lane) {
 #pragma clang fp contract(off)
   constexpr int HDP = HD / 2, HDG = HD / kGroup;
   const AppendArgs& w = a.wr;
   const int P = g.page, ppg = kGroup / P;
   const int start = step_len(a, b) - 1;
   const int old0 = split_old_tokens(start, g.residual), r0 = start - old0;  // r0 = R + 31
-  uint16_t* xs = (is_v ? w.v_scr : w.k_scr) + (int64_t)b * w.scr_stride + (int64_t)h * g.rs * HD;
-  const uint16_t* nx = (is_v ? w.new_v : w.new_k) + (int64_t)b * w.new_stride + (int64_t)h * HD;
+  uint16_t* xs = (is_v ? w.v_scr : w.k_scr) + (int64_t)b * w.scr_stride + (int64_t)h * g.rs * HD +
+                 kGroup * q;
+  const uint16_t* nx =
+      (is_v ? w.new_v : w.new_k) + (int64_t)b * w.new_stride + (int64_t)h * HD + kGroup * q;
   const int fp = (old0 / kGroup) * ppg;  // the group's first logical page
   const bool table_ok = fp + ppg <= g.max_pages;
   int p0 = -1, p1 = -1;
@@ -1273,121 +1319,136 @@ __device__ __attribute__((always_inline)) inline void step_age_out(const KiviGeo
     p0 = bt[fp];
     p1 = ppg == 2 ? bt[fp + 1] : p0;
   }
-  auto phys_ok = [&](int p) { return p >= 0 && p < g.num_pages; };
+  auto phys_ok = [&](int p) { return table_ok && p >= 0 && p < g.num_pages; };
   if (!is_v) {
-    // K: lane = channel pair (2 lane, 2 lane + 1), all 32 tokens
-    if (lane < HDP) {
-      uint32_t x[kGroup];
+    // K: lane = (channel pair pr of the slice's 16, token quarter tq): the
+    // pair's min / max over its 8 tokens, merged over the 4 quarters
+    const int pr = lane >> 2, tq = lane & 3, t0 = 8 * tq;
+    uint32_t x[8];
 #pragma unroll
-      for (int t = 0; t < kGroup; ++t) x[t] = *(const uint32_t*)(xs + t * HD + 2 * lane);
-      float mn0 = h2f((uint16_t)x[0]), mx0 = mn0, mn1 = h2f((uint16_t)(x[0] >> 16)), mx1 = mn1;
+    for (int t = 0; t < 8; ++t) x[t] = *(const uint32_t*)(xs + (t0 + t) * HD + 2 * pr);
+    float mn0 = h2f((uint16_t)x[0]), mx0 = mn0, mn1 = h2f((uint16_t)(x[0] >> 16)), mx1 = mn1;
 #pragma unroll
-      for (int t = 1; t < kGroup; ++t) {
-        const float v0 = h2f((uint16_t)x[t]), v1 = h2f((uint16_t)(x[t] >> 16));
-        mn0 = min_num(mn0, v0);
-        mx0 = max_num(mx0, v0);
-        mn1 = min_num(mn1, v1);
-        mx1 = max_num(mx1, v1);
+    for (int t = 1; t < 8; ++t) {
+      const float v0 = h2f((uint16_t)x[t]), v1 = h2f((uint16_t)(x[t] >> 16));
+      mn0 = min_num(mn0, v0);
+      mx0 = max_num(mx0, v0);
+      mn1 = min_num(mn1, v1);
+      mx1 = max_num(mx1, v1);
+    }
+#pragma unroll
+    for (int off = 1; off < 4; off <<= 1) {
+      mn0 = min_num(mn0, __shfl_xor(mn0, off, 64));
+      mx0 = max_num(mx0, __shfl_xor(mx0, off, 64));
+      mn1 = min_num(mn1, __shfl_xor(mn1, off, 64));
+      mx1 = max_num(mx1, __shfl_xor(mx1, off, 64));
+    }
+    float s0 = (mx0 - mn0) / 15.0f, s1 = (mx1 - mn1) / 15.0f;
+    if (!(s0 > 0.0f)) s0 = 1.0f;
+    if (!(s1 > 0.0f)) s1 = 1.0f;
+    const int d0 = kGroup * q + 2 * pr;  // channel of the pair's low nibble
+    if (tq == 0) {
+      const uint32_t sc = (uint32_t)f2h(s0) | ((uint32_t)f2h(s1) << 16);
+      const uint32_t zr = (uint32_t)f2h(mn0) | ((uint32_t)f2h(mn1) << 16);
+      for (int pg = 0; pg < ppg; ++pg) {  // K scales live in every page of the group
+        const int phys = pg == 0 ? p0 : p1;
+        if (!phys_ok(phys)) continue;
+        const int64_t base = ((int64_t)phys * g.nkv + h) * HD + d0;
+        st_dev((uint32_t*)(w.k_scale + base), sc);
+        st_dev((uint32_t*)(w.k_zero + base), zr);
       }
-      float s0 = (mx0 - mn0) / 15.0f, s1 = (mx1 - mn1) / 15.0f;
-      if (!(s0 > 0.0f)) s0 = 1.0f;
-      if (!(s1 > 0.0f)) s1 = 1.0f;
-      if (table_ok) {
-        const uint32_t sc = (uint32_t)f2h(s0) | ((uint32_t)f2h(s1) << 16);
-        const uint32_t zr = (uint32_t)f2h(mn0) | ((uint32_t)f2h(mn1) << 16);
-        for (int pg = 0; pg < ppg; ++pg) {  // K scales live in every page of the group
-          const int phys = pg == 0 ? p0 : p1;
-          if (!phys_ok(phys)) continue;
-          const int64_t base = ((int64_t)phys * g.nkv + h) * HD + 2 * lane;
-          *(uint32_t*)(w.k_scale + base) = sc;
-          *(uint32_t*)(w.k_zero + base) = zr;
-        }
+    }
 #pragma unroll
-        for (int t = 0; t < kGroup; ++t) {
-          const int phys = t < P ? p0 : p1;
-          const int c0 = clamp_code((h2f((uint16_t)x[t]) - mn0) / s0);
-          const int c1 = clamp_code((h2f((uint16_t)(x[t] >> 16)) - mn1) / s1);
-          if (phys_ok(phys))
-            w.k_code[(((int64_t)phys * g.nkv + h) * P + t % P) * HDP + lane] =
-                (uint8_t)((c0 & 0x0f) | ((c1 & 0x0f) << 4));
-        }
-      }
+    for (int t = 0; t < 8; ++t) {
+      const int tok = t0 + t, phys = tok < P ? p0 : p1;
+      const int c0 = clamp_code((h2f((uint16_t)x[t]) - mn0) / s0);
+      const int c1 = clamp_code((h2f((uint16_t)(x[t] >> 16)) - mn1) / s1);
+      if (phys_ok(phys))
+        st_dev(w.k_code + (((int64_t)phys * g.nkv + h) * P + tok % P) * HDP + d0 / 2,
+               (uint8_t)((c0 & 0x0f) | ((c1 & 0x0f) << 4)));
     }
   } else {
-    // V: (token t, 32-channel group cg) per lane and pass
-    for (int it = lane; it < kGroup * HDG; it += 64) {
-      const int t = it / HDG, cg = it % HDG;
-      const uint16_t* row = xs + t * HD + cg * kGroup;
-      u32x4 v[4];
+    // V: lane = (token t, half hf of the slice's 32 channels); min / max over
+    // 16 channels, merged with the other half
+    const int t = lane >> 1, hf = lane & 1;
+    const uint16_t* row = xs + t * HD + 16 * hf;
+    const u32x4 v0 = *(const u32x4*)row, v1 = *(const u32x4*)(row + 8);
+    auto ch = [&](int k) -> float {  // channel k of the lane's 16
+      const u32x4& v = k < 8 ? v0 : v1;
+      return h2f((uint16_t)(v[(k % 8) / 2] >> (16 * (k & 1))));
+    };
+    float mn = ch(0), mx = mn;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) v[q] = *(const u32x4*)(row + 8 * q);
-      float mn = h2f((uint16_t)v[0][0]), mx = mn;
+    for (int k = 1; k < 16; ++k) {
+      mn = min_num(mn, ch(k));
+      mx = max_num(mx, ch(k));
+    }
+    mn = min_num(mn, __shfl_xor(mn, 1, 64));
+    mx = max_num(mx, __shfl_xor(mx, 1, 64));
+    float sv = (mx - mn) / 15.0f;
+    if (!(sv > 0.0f)) sv = 1.0f;
+    u32x2 codes;
 #pragma unroll
-      for (int k = 1; k < kGroup; ++k) {
-        const float x = h2f((uint16_t)(v[k / 8][(k % 8) / 2] >> (16 * (k & 1))));
-        mn = min_num(mn, x);
-        mx = max_num(mx, x);
-      }
-      float sv = (mx - mn) / 15.0f;
-      if (!(sv > 0.0f)) sv = 1.0f;
-      u32x4 codes;
+    for (int wd = 0; wd < 2; ++wd) {
+      uint32_t word = 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const int ch = 8 * q + k;
-          const float x = h2f((uint16_t)(v[ch / 8][(ch % 8) / 2] >> (16 * (ch & 1))));
-          word |= (uint32_t)clamp_code((x - mn) / sv) << (4 * k);
-        }
-        codes[q] = word;
-      }
-      const int phys = t < P ? p0 : p1;
-      if (table_ok && phys_ok(phys)) {
-        const int64_t tok = ((int64_t)phys * g.nkv + h) * P + t % P;
-        *(u32x4*)(w.v_code + tok * HDP + cg * (kGroup / 2)) = codes;
-        w.v_scale[tok * HDG + cg] = f2h(sv);
-        w.v_zero[tok * HDG + cg] = f2h(mn);
+      for (int k = 0; k < 8; ++k) word |= (uint32_t)clamp_code((ch(8 * wd + k) - mn) / sv) << (4 * k);
+      codes[wd] = word;
+    }
+    const int phys = t < P ? p0 : p1;
+    if (phys_ok(phys)) {
+      const int64_t tok = ((int64_t)phys * g.nkv + h) * P + t % P;
+      st_dev((uint64_t*)(w.v_code + tok * HDP + q * (kGroup / 2) + 8 * hf),
+             __builtin_bit_cast(uint64_t, codes));
+      if (hf == 0) {
+        st_dev(w.v_scale + tok * HDG + q, f2h(sv));
+        st_dev(w.v_zero + tok * HDG + q, f2h(mn));
       }
     }
   }
-  // shift: rows [0, R - 1) <- rows [32, R + 31) in forward chunks, every load
-  // of a chunk before its stores (a chunk's sources lie above every row it
-  // or an earlier chunk stores); the quantisation above read rows 0..31 first
-  constexpr int V16 = HD / 8;  // 16-byte pieces per row
-  const int units = (g.residual - 1) * V16;
-  constexpr int CH = 8;  // pieces per lane and chunk
-  for (int u0 = 0; u0 < units; u0 += 64 * CH) {
-    u32x4 buf[CH];
+  // shift the slice: rows [0, R - 1) <- rows [32, R + 31), four 16-byte
+  // pieces per row, in chunks of 8 pieces per lane.  Within a chunk store k
+  // writes rows that no later load of any chunk reads (sources lie 32 rows
+  // above), and the quantisation above read rows 0..31 first.
+  const int units = (g.residual - 1) * 4;
+  for (int u0 = 0; u0 < units; u0 += 64 * 8) {
+    u32x4 buf[8];
 #pragma unroll
-    for (int k = 0; k < CH; ++k) {
+    for (int k = 0; k < 8; ++k) {
       const int u = min(u0 + lane + 64 * k, units - 1);
-      buf[k] = *(const u32x4*)(xs + (int64_t)(u / V16 + kGroup) * HD + 8 * (u % V16));
+      buf[k] = *(const u32x4*)(xs + (int64_t)(u / 4 + kGroup) * HD + 8 * (u % 4));
     }
 #pragma unroll
-    for (int k = 0; k < CH; ++k) {
+    for (int k = 0; k < 8; ++k) {
       const int u = u0 + lane + 64 * k;
-      if (u < units) *(u32x4*)(xs + (int64_t)(u / V16) * HD + 8 * (u % V16)) = buf[k];
+      if (u < units)
+        st_agent4((float*)(xs + (int64_t)(u / 4) * HD + 8 * (u % 4)),
+                  __builtin_bit_cast(floatx4, buf[k]));
     }
   }
-  // the new token: row R - 1 (live) and row r0 (the reference's stale copy)
-  if (lane < 2 * V16) {
-    const int row = lane < V16 ? g.residual - 1 : r0, piece = lane % V16;
-    *(u32x4*)(xs + (int64_t)row * HD + 8 * piece) = *(const u32x4*)(nx + 8 * piece);
+  // the new token's slice: row R - 1 (live) and row r0 (the reference's stale copy)
+  if (lane < 8) {
+    const int row = lane < 4 ? g.residual - 1 : r0, piece = lane % 4;
+    st_agent4((float*)(xs + (int64_t)row * HD + 8 * piece),
+              __builtin_bit_cast(floatx4, *(const u32x4*)(nx + 8 * piece)));
   }
-  // the stores above reach the point of coherence of every XCD before the flag
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  // every store above is device-scope (the readers' loads are too): complete
+  // before the flag
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   if (lane == 0)
-    __hip_atomic_store(a.ws_wflag + 2 * ((int64_t)b * g.nkv + h) + (is_v ? 1 : 0), a.epoch,
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.ws_wflag + step_flags<HD>() * ((int64_t)b * g.nkv + h) +
+                           (is_v ? HDG : 0) + q,
+                       a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Writer wavefront wi of a.writer_waves: first the age-out items (sequence
 // rank among the aging ones, kv head, K | V) in turn, then the plain appends
 // of the other (sequence, kv head) pairs.
 template <int HD>
-__device__ __attribute__((always_inline)) inline void step_writer(const KiviGeo& g, const DecodeArgs& a, int wi,
+__device__ __attribute__((always_inline)) inline uint64_t step_writer(const KiviGeo& g, const DecodeArgs& a, int wi,
                                                                 int lane) {
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  uint64_t tf = t0;  // profiling: the end of its last age-out item
   const int NW = a.writer_waves, NKV = g.nkv;
   int rank0 = 0;  // aging sequences before this 64-sequence window
   for (int base = 0; base < a.batch; base += 64) {
@@ -1398,9 +1459,14 @@ __device__ __attribute__((always_inline)) inline void step_writer(const KiviGeo&
     while (m) {
       const int b = base + __builtin_ctzll(m);
       m &= m - 1;
-      for (int k = 0; k < 2 * NKV; ++k) {
-        const int item = rank * 2 * NKV + k;
-        if (item % NW == wi) step_age_out<HD>(g, a, b, k >> 1, k & 1, lane);
+      constexpr int F = step_flags<HD>();  // items per (sequence, kv head)
+      for (int k = 0; k < F * NKV; ++k) {
+        const int item = rank * F * NKV + k;
+        if (item % NW == wi) {
+          const int hh = k / F, f = k % F;
+          step_age_out<HD>(g, a, b, hh, f >= F / 2, f % (F / 2), lane);
+          tf = __builtin_amdgcn_s_memrealtime();
+        }
       }
       ++rank;
     }
@@ -1422,6 +1488,7 @@ __device__ __attribute__((always_inline)) inline void step_writer(const KiviGeo&
       *(u32x4*)(xs + (int64_t)r0 * HD + 8 * piece) = *(const u32x4*)(nx + 8 * piece);
     }
   }
+  return tf - t0;
 }
 
 // One run of the stream: units [x0, x1) of the concatenated (sequence, kv
@@ -1467,298 +1534,350 @@ __device__ __attribute__((always_inline)) inline uint64_t stream_run(
   };
   int kvh = (int)((x0 - sp.start) / sp.units);
   int u = (int)((x0 - sp.start) % sp.units);  // unit offset inside the segment
-  int64_t x = x0;
+  int64_t x = x0, xe = x1;                  // the current pass: [x, xe)
+  // fused step: a run whose first segment ages a group out would wait for the
+  // writer at its very start; when the run goes on into further segments it
+  // decodes those first and that segment last (two passes), by which time
+  // the writer is done
+  int64_t x_rot = -1;
+  SeqSpan sp_rot = sp;
+  int kvh_rot = kvh, u_rot = u;
+  if constexpr (FUSED) {
+    const int64_t seg_end = x0 + (sp.units - u);
+    if (seg_end < x1) {
+      int ov0, n0_;
+      seq_tiles(g, a, sp.b, &ov0, &n0_);
+      const int L0 = step_len(a, sp.b);
+      if (step_ages(g, L0) && ov0 == split_old_tokens(L0, g.residual)) {
+        x_rot = x0;
+        xe = seg_end;  // the end of the rotated-away pass, kept below
+        x = seg_end;
+        u = 0;
+        if (++kvh == NKV) {
+          kvh = 0;
+          sp.b += 1;
+        }
+        first_seg = false;
+      }
+    }
+  }
+  const int64_t x_rot_end = xe;
+  if (x_rot >= 0) xe = x1;
   int64_t cut_first = -1, cut_last = -1;  // pieces this run leaves as partials
   uint64_t t_first = 0;                   // profiling: first group in LDS
-  while (x < x1) {
-    const int b = sp.b, h = kvh;
-    int ov = first_ov, n = first_n, T = first_T;
-    if (!first_seg) T = seq_tiles(g, a, b, &ov, &n);
-    first_seg = false;
-    const int nq = ov / kGroup;
-    const int u_end = (int)min((int64_t)(nq + kResidualUnits * (T - nq)), u + (x1 - x));
-    const int t_beg = tile_at(u, nq), t_fin = tile_at(u_end, nq);
-    x += u_end - u;
-    u = 0;
-    if (++kvh == NKV) {
-      kvh = 0;
-      sp.b += 1;
-    }
-    // the run starts inside this segment's last residual tile, which the
-    // previous wavefront owns: nothing here (no partial, no map entry)
-    if (t_beg >= t_fin) continue;
-
-    // fused step: a segment whose sequence ages a group out reads its new
-    // group (tile g_age) and its residual rows only after the writer's two
-    // flags; in the others the residual row new_row (the new token) comes
-    // from NEW_K / NEW_V, never from the scratch the writer is storing to
-    int g_age = 0x7fffffff, new_row = -1;
-    bool ages = false, aging = false, waited = false;
-    if constexpr (FUSED) {
-      const int Lb = step_len(a, b);
-      ages = step_ages(g, Lb);
-      aging = ages && ov == split_old_tokens(Lb, g.residual);
-      if (aging)
-        g_age = ov / kGroup - 1;
-      else if (Lb == n && n > ov)
-        new_row = n - ov - 1;
-    }
-    auto wait_new = [&]() {
-      if (waited) return;
-      waited = true;
-      if (lane == 0) {
-        const uint64_t* f = a.ws_wflag + 2 * ((int64_t)b * NKV + h);
-        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-        bool late = false;
-        while (ld_agent(f) != a.epoch || ld_agent(f + 1) != a.epoch) {
-          if (__builtin_amdgcn_s_memrealtime() - t0 > a.merge_timeout) {
-            late = true;
-            break;
-          }
-          __builtin_amdgcn_s_sleep(2);
-        }
-        if (late && a.status)
-          __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  uint64_t t_wait = 0;                    // profiling (fused step): ticks waited for the writer
+  for (;;) {
+    while (x < xe) {
+      const int b = sp.b, h = kvh;
+      int ov = first_ov, n = first_n, T = first_T;
+      if (!first_seg) T = seq_tiles(g, a, b, &ov, &n);
+      first_seg = false;
+      const int nq = ov / kGroup;
+      const int u_end = (int)min((int64_t)(nq + kResidualUnits * (T - nq)), u + (xe - x));
+      const int t_beg = tile_at(u, nq), t_fin = tile_at(u_end, nq);
+      x += u_end - u;
+      u = 0;
+      if (++kvh == NKV) {
+        kvh = 0;
+        sp.b += 1;
       }
-      // the writer's stores (another XCD's L2 wrote them back) before any load
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    };
+      // the run starts inside this segment's last residual tile, which the
+      // previous wavefront owns: nothing here (no partial, no map entry)
+      if (t_beg >= t_fin) continue;
 
-    // ---- quantised groups: a ring of S LDS stages, S - 1 in flight ----
-    const int tq_end = min(t_fin, ov / kGroup);
-    // read-only for the whole launch: the constant address space lets the
-    // wave-uniform page reads be scalar loads (lgkmcnt, not vmcnt)
-    const __attribute__((address_space(4))) int32_t* bt =
-        (const __attribute__((address_space(4))) int32_t*)(a.block_tables +
-                                                           (int64_t)b * a.bt_stride);
-    const StageBases sb = stage_bases<HD, P>(a, NKV, h, lane);
-    auto page = [&](int tile, int k) -> uint32_t {
-      return (uint32_t)bt[tile * C::PPG + (C::PPG == 2 ? k : 0)];
-    };
-    uint32_t n0 = 0, n1 = 0;  // pages of group i + S - 1, read one group early
-    if (t_beg < tq_end) {
+      // fused step: a segment whose sequence ages a group out reads its new
+      // group (tile g_age) and its residual rows only after the writer's two
+      // flags; in the others the residual row new_row (the new token) comes
+      // from NEW_K / NEW_V, never from the scratch the writer is storing to
+      int g_age = 0x7fffffff, new_row = -1;
+      bool ages = false, aging = false, waited = false;
       if constexpr (FUSED) {
-        if (g_age >= t_beg && g_age < t_beg + S - 1 && g_age < tq_end) wait_new();
+        const int Lb = step_len(a, b);
+        ages = step_ages(g, Lb);
+        aging = ages && ov == split_old_tokens(Lb, g.residual);
+        if (aging)
+          g_age = ov / kGroup - 1;
+        else if (Lb == n && n > ov)
+          new_row = n - ov - 1;
       }
-      wait_vm<0>();  // the counts below see only this segment's DMAs
+      auto wait_new = [&]() {
+        if (waited) return;
+        waited = true;
+        if (lane == 0) {
+          constexpr int F = step_flags<HD>();
+          const uint64_t* f = a.ws_wflag + F * ((int64_t)b * NKV + h);
+          const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+          bool late = false;
+          auto ready = [&]() {
+            bool r = true;
 #pragma unroll
-      for (int k = 0; k < S - 1; ++k)
-        if (t_beg + k < tq_end)
-          load_stage<HD, P>(&ring[k], sb, page(t_beg + k, 0), page(t_beg + k, 1), lane);
-      if (t_beg + S - 1 < tq_end) {
-        n0 = page(t_beg + S - 1, 0);
-        n1 = page(t_beg + S - 1, 1);
-      }
-    }
-
-    // ---- Q operands and softmax state (the loads overlap the first DMAs) ----
-    SegCtx<HD> q;
-    const uint16_t* qh = a.q + (int64_t)b * a.q_stride + (int64_t)h * G * HD;
-    // lane offsets from an opaque lane id (hoisted out of the segment loop,
-    // they would hold 64-bit registers through the whole run)
-    int lq = lane;
-    asm volatile("" : "+v"(lq));
-    const int hq = PACK ? (lq & 7) : (lq & 15);  // packed: columns c and c + 8 share head c
-    const int jq = lq >> 4;
-    uint16_t* qrow = &qrows[hq * QROW + jq * (HD / 4)];
-    q.qn = (const uint8_t*)qrow;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (hq < G) {
-        v = *(const u32x4*)(qh + hq * HD + jq * (HD / 4) + 8 * ks);
-        *(u32x4*)(qrow + 8 * ks) = v;  // the same words from columns c and c + 8
-      }
-      const half8_t div = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)0.0625f, (_Float16)0.0625f,
-                           (_Float16)1.0f, (_Float16)1.0f, (_Float16)0.0625f, (_Float16)0.0625f};
-      q.qp[ks] = as_h8(perm_pairs(v)) * div;
-    }
-    WaveState<HD> st;
-#pragma unroll
-    for (int nt = 0; nt < CPL; ++nt) st.o[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    st.ob = floatx4{0.f, 0.f, 0.f, 0.f};
-    st.m = -1.0e30f;
-
-    const int r_beg = max(t_beg, ov / kGroup);  // first fp16 residual tile
-    if (t_beg < tq_end) {
-      const LaneMap lm = lane_map<HD, P>(lane);
-      int slot = 0;
-      for (int i = t_beg; i < tq_end; ++i) {
-        const int ahead = slot == 0 ? S - 1 : slot - 1;  // (slot + S - 1) % S
-        if (i + S - 1 < tq_end) {
-          if constexpr (FUSED) {
-            if (i + S - 1 == g_age) wait_new();
-          }
-          load_stage<HD, P>(&ring[ahead], sb, n0, n1, lane);
-          if (i + S < tq_end) {
-            n0 = page(i + S, 0);
-            n1 = page(i + S, 1);
-          }
-          wait_vm<(S - 1) * L>();
-        } else {
-          wait_stages<L, S>(tq_end - 1 - i);
-        }
-        if (a.stamps && t_first == 0) t_first = __builtin_amdgcn_s_memrealtime();
-        const VData vd = load_v<HD, P>(&ring[slot], lm);
-        const half8_t pa = qk_softmax<HD, P, PACK>(st, q, &ring[slot], lm, nb, sscale, lane);
-        st.ob = mfma(pa, as_h8(vd.vz4), st.ob);  // sum_t P z_t
-        pv_group<HD>(st, pa, vd, nb, big_scales(vd), false, PStash(nullptr));
-        // the range test comes last, so the steps above stay one block for
-        // the scheduler (a branch between them costs the common case ~15%)
-        if (__builtin_expect(wide_group<HD>(&ring[slot], lane), 0))
-          exact_fix_group<HD, P, PACK>(st, q, &ring[slot], lm, nb, sscale, lane, pa, vd);
-        slot = slot == S - 1 ? 0 : slot + 1;
-        progress(1);
-      }
-    }
-
-    // ---- fp16 residual tiles (all loads of a tile issued before its first use) ----
-    if constexpr (FUSED) {
-      if (aging && r_beg < t_fin) wait_new();
-    }
-    for (int i = r_beg; i < t_fin; ++i) {
-      ResTile<HD> cur = load_res<HD, FUSED>(a, g, b, h, ov, n, i, lane, new_row);
-      const int tn = min(kGroup, n - i * kGroup);  // 0 only for an empty sequence
-      floatx4 sres[2];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        sres[tt] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) sres[tt] = mfma(as_h8(cur.kv[tt][ks]), q.n(ks), sres[tt]);
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii)
-          if (8 * j + 4 * tt + ii >= tn) sres[tt][ii] = -INFINITY;
-      }
-      // rows past the end carry P = 0 but must not carry NaN/Inf garbage
-#pragma unroll
-      for (int r = 0; r < 8; ++r)
-        if (8 * j + r >= tn) cur.vr[r] = typename ResTile<HD>::vrow_t(0u);
-      // P also goes to LDS in fp32 (slot 0 is idle: every stage DMA has
-      // landed), for the exact correction of values above kFastRange
-      const PStash ps(ring[0].k);
-      const half8_t prh = softmax_tile<HD>(st, sres[0], sres[1], sscale, 0.0f, j, true, ps);
-      half2_t vmax = {(_Float16)0.0f, (_Float16)0.0f};
-#pragma unroll
-      for (int r = 0; r < 8; ++r)
-#pragma unroll
-        for (int e = 0; e < (int)(sizeof(cur.vr[0]) / 4); ++e)
-          vmax = __builtin_elementwise_max(vmax, __builtin_elementwise_abs(as_h2(cur.vr[r][e])));
-      const bool wide = __builtin_amdgcn_ballot_w64((float)vmax[0] > kFastRange ||
-                                                    (float)vmax[1] > kFastRange) != 0;
-      // B operand of output columns nt: the tile rows' channels 16 nt + c
-      auto cols = [&](int nt) {
-        u32x4 vb;
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          const uint32_t va = cur.vr[2 * qq][nt >> 1], vb2 = cur.vr[2 * qq + 1][nt >> 1];
-          vb[qq] = (nt & 1) ? __builtin_amdgcn_perm(vb2, va, 0x07060302u)
-                            : __builtin_amdgcn_perm(vb2, va, 0x05040100u);
-        }
-        return as_h8(vb);
-      };
-      // A residual tile (a few per segment, not the hot loop) takes one
-      // arithmetic or the other, chosen before its PV step: a correction
-      // after the fp16 step would turn an infinite value into inf - inf.
-      if (__builtin_expect(wide, 0)) {  // fp32 P against the (exact) fp16 values
-#pragma unroll
-        for (int nt = 0; nt < CPL; ++nt) {
-          const half8_t vh = cols(nt);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) st.o[nt] = mfma32(ps.get(i), (float)vh[i], st.o[nt]);
-        }
-        // Sigma P into the sum columns; the column test is redone from an
-        // opaque lane id, not kept live
-        int ln = lane;
-        asm volatile("" : "+v"(ln));
-        const float one = sum_lane<HD>(ln & 15) ? 1.0f : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) st.ob = mfma32(ps.get(i), one, st.ob);
-      } else {
-#pragma unroll
-        for (int nt = 0; nt < CPL; ++nt) st.o[nt] = mfma(prh, cols(nt), st.o[nt]);
-        const uint32_t one2 = sum_col ? 0x3C003C00u : 0u;  // Sigma P into the sum columns
-        st.ob = mfma(prh, as_h8(u32x4{one2, one2, one2, one2}), st.ob);
-      }
-      progress(kResidualUnits);
-    }
-
-    // ---- segment output: O directly, or a partial for the merge workgroups ----
-    // row sums: Sigma P of O row 4j + i sits in the sum column C1 of row
-    // block j; a sum lane takes its group's Sigma P z from its left neighbour
-    const bool whole = (t_beg == 0 && t_fin == T);
-    const int64_t piece = (int64_t)b * NKV + h + w;
-    float rowscale[4], zsum[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float li = __shfl(st.ob[i], 16 * j + C1, 64);
-      const float left = __shfl(st.ob[i], lane - 1, 64);
-      zsum[i] = sum_col ? left : st.ob[i];
-      rowscale[i] = whole ? 1.0f / fmaxf(li, 1.0e-30f) : 1.0f;
-    }
-    float* dst = whole ? a.out + (int64_t)b * a.out_stride + (int64_t)h * G * HD
-                       : a.ws_acc + piece * G * HD;
-    // the lane's output offset, computed here: hoisted out of the segment
-    // loop it would hold two registers for the whole run
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
-    const int lane_off = (ln >> 4) * 4 * HD + CPL * (ln & 15);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 4 * j + i;
-      if (row < G) {
-        float v[CPL];
-#pragma unroll
-        for (int nt = 0; nt < CPL; ++nt) v[nt] = (st.o[nt][i] + zsum[i]) * rowscale[i];
-        float* p = dst + lane_off + i * HD;
-        if (whole) {
-#pragma unroll
-          for (int q4 = 0; q4 < CPL / 4; ++q4)
-            *(floatx4*)(p + 4 * q4) =
-                floatx4{v[4 * q4], v[4 * q4 + 1], v[4 * q4 + 2], v[4 * q4 + 3]};
-        } else if (CPL == 4) {  // read by a merge wavefront, possibly on another XCD
-          st_agent4(p, floatx4{v[0], v[1], v[2], v[3]});
-        } else {
-          // agent-scope stores bypass the L2, so each instruction should
-          // write whole sectors: lane c of the row's 16 takes floats
-          // 4c .. 4c + 3 and then 64 + 4c .. 64 + 4c + 3 (held by lanes c / 2
-          // and 8 + c / 2, half c % 2), two 256-byte contiguous stores
-          float* row_base = dst + (((ln >> 4) << 2) + i) * HD;
-          const int cl = ln & 15, src0 = (ln & 48) + (cl >> 1), hi = cl & 1;
-#pragma unroll
-          for (int part = 0; part < 2; ++part) {
-            const int src = src0 + 8 * part;
-            floatx4 o;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float lo_half = __shfl(v[e], src, 64), hi_half = __shfl(v[4 + e], src, 64);
-              o[e] = hi ? hi_half : lo_half;
+            for (int k = 0; k < F; ++k) r = r && ld_agent(f + k) == a.epoch;
+            return r;
+          };
+          while (!ready()) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > a.merge_timeout) {
+              late = true;
+              break;
             }
-            st_agent4(row_base + 64 * part + 4 * cl, o);
+            __builtin_amdgcn_s_sleep(2);
+          }
+          if (a.stamps) t_wait += __builtin_amdgcn_s_memrealtime() - t0;
+          if (late && a.status)
+            __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        // the writer stored with device-scope stores; the segment's new group
+        // and residual rows are read with device-scope loads (COH)
+      };
+
+      // ---- quantised groups: a ring of S LDS stages, S - 1 in flight ----
+      const int tq_end = min(t_fin, ov / kGroup);
+      // read-only for the whole launch: the constant address space lets the
+      // wave-uniform page reads be scalar loads (lgkmcnt, not vmcnt)
+      const __attribute__((address_space(4))) int32_t* bt =
+          (const __attribute__((address_space(4))) int32_t*)(a.block_tables +
+                                                             (int64_t)b * a.bt_stride);
+      const StageBases sb = stage_bases<HD, P>(a, NKV, h, lane);
+      auto page = [&](int tile, int k) -> uint32_t {
+        return (uint32_t)bt[tile * C::PPG + (C::PPG == 2 ? k : 0)];
+      };
+      uint32_t n0 = 0, n1 = 0;  // pages of group i + S - 1, read one group early
+      if (t_beg < tq_end) {
+        if constexpr (FUSED) {
+          if (g_age >= t_beg && g_age < t_beg + S - 1 && g_age < tq_end) wait_new();
+        }
+        wait_vm<0>();  // the counts below see only this segment's DMAs
+#pragma unroll
+        for (int k = 0; k < S - 1; ++k)
+          if (t_beg + k < tq_end)
+            if (FUSED && t_beg + k == g_age)
+              load_stage<HD, P, true>(&ring[k], sb, page(t_beg + k, 0), page(t_beg + k, 1), lane);
+            else
+              load_stage<HD, P>(&ring[k], sb, page(t_beg + k, 0), page(t_beg + k, 1), lane);
+        if (t_beg + S - 1 < tq_end) {
+          n0 = page(t_beg + S - 1, 0);
+          n1 = page(t_beg + S - 1, 1);
+        }
+      }
+
+      // ---- Q operands and softmax state (the loads overlap the first DMAs) ----
+      SegCtx<HD> q;
+      const uint16_t* qh = a.q + (int64_t)b * a.q_stride + (int64_t)h * G * HD;
+      // lane offsets from an opaque lane id (hoisted out of the segment loop,
+      // they would hold 64-bit registers through the whole run)
+      int lq = lane;
+      asm volatile("" : "+v"(lq));
+      const int hq = PACK ? (lq & 7) : (lq & 15);  // packed: columns c and c + 8 share head c
+      const int jq = lq >> 4;
+      uint16_t* qrow = &qrows[hq * QROW + jq * (HD / 4)];
+      q.qn = (const uint8_t*)qrow;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (hq < G) {
+          v = *(const u32x4*)(qh + hq * HD + jq * (HD / 4) + 8 * ks);
+          *(u32x4*)(qrow + 8 * ks) = v;  // the same words from columns c and c + 8
+        }
+        const half8_t div = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)0.0625f, (_Float16)0.0625f,
+                             (_Float16)1.0f, (_Float16)1.0f, (_Float16)0.0625f, (_Float16)0.0625f};
+        q.qp[ks] = as_h8(perm_pairs(v)) * div;
+      }
+      WaveState<HD> st;
+#pragma unroll
+      for (int nt = 0; nt < CPL; ++nt) st.o[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      st.ob = floatx4{0.f, 0.f, 0.f, 0.f};
+      st.m = -1.0e30f;
+
+      const int r_beg = max(t_beg, ov / kGroup);  // first fp16 residual tile
+      if (t_beg < tq_end) {
+        const LaneMap lm = lane_map<HD, P>(lane);
+        int slot = 0;
+        for (int i = t_beg; i < tq_end; ++i) {
+          const int ahead = slot == 0 ? S - 1 : slot - 1;  // (slot + S - 1) % S
+          if (i + S - 1 < tq_end) {
+            if (FUSED && i + S - 1 == g_age) {
+              wait_new();
+              load_stage<HD, P, true>(&ring[ahead], sb, n0, n1, lane);
+            } else {
+              load_stage<HD, P>(&ring[ahead], sb, n0, n1, lane);
+            }
+            if (i + S < tq_end) {
+              n0 = page(i + S, 0);
+              n1 = page(i + S, 1);
+            }
+            wait_vm<(S - 1) * L>();
+          } else {
+            wait_stages<L, S>(tq_end - 1 - i);
+          }
+          if (a.stamps && t_first == 0) t_first = __builtin_amdgcn_s_memrealtime();
+          const VData vd = load_v<HD, P>(&ring[slot], lm);
+          const half8_t pa = qk_softmax<HD, P, PACK>(st, q, &ring[slot], lm, nb, sscale, lane);
+          st.ob = mfma(pa, as_h8(vd.vz4), st.ob);  // sum_t P z_t
+          pv_group<HD>(st, pa, vd, nb, big_scales(vd), false, PStash(nullptr));
+          // the range test comes last, so the steps above stay one block for
+          // the scheduler (a branch between them costs the common case ~15%)
+          if (__builtin_expect(wide_group<HD>(&ring[slot], lane), 0))
+            exact_fix_group<HD, P, PACK>(st, q, &ring[slot], lm, nb, sscale, lane, pa, vd);
+          slot = slot == S - 1 ? 0 : slot + 1;
+          progress(1);
+        }
+      }
+
+      // ---- fp16 residual tiles (all loads of a tile issued before its first use) ----
+      if constexpr (FUSED) {
+        if (aging && r_beg < t_fin) wait_new();
+      }
+      for (int i = r_beg; i < t_fin; ++i) {
+        ResTile<HD> cur =
+            (FUSED && aging) ? load_res<HD, FUSED, true>(a, g, b, h, ov, n, i, lane, new_row)
+                             : load_res<HD, FUSED, false>(a, g, b, h, ov, n, i, lane, new_row);
+        const int tn = min(kGroup, n - i * kGroup);  // 0 only for an empty sequence
+        floatx4 sres[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          sres[tt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) sres[tt] = mfma(as_h8(cur.kv[tt][ks]), q.n(ks), sres[tt]);
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii)
+            if (8 * j + 4 * tt + ii >= tn) sres[tt][ii] = -INFINITY;
+        }
+        // rows past the end carry P = 0 but must not carry NaN/Inf garbage
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+          if (8 * j + r >= tn) cur.vr[r] = typename ResTile<HD>::vrow_t(0u);
+        // P also goes to LDS in fp32 (slot 0 is idle: every stage DMA has
+        // landed), for the exact correction of values above kFastRange
+        const PStash ps(ring[0].k);
+        const half8_t prh = softmax_tile<HD>(st, sres[0], sres[1], sscale, 0.0f, j, true, ps);
+        half2_t vmax = {(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+          for (int e = 0; e < (int)(sizeof(cur.vr[0]) / 4); ++e)
+            vmax = __builtin_elementwise_max(vmax, __builtin_elementwise_abs(as_h2(cur.vr[r][e])));
+        const bool wide = __builtin_amdgcn_ballot_w64((float)vmax[0] > kFastRange ||
+                                                      (float)vmax[1] > kFastRange) != 0;
+        // B operand of output columns nt: the tile rows' channels 16 nt + c
+        auto cols = [&](int nt) {
+          u32x4 vb;
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq) {
+            const uint32_t va = cur.vr[2 * qq][nt >> 1], vb2 = cur.vr[2 * qq + 1][nt >> 1];
+            vb[qq] = (nt & 1) ? __builtin_amdgcn_perm(vb2, va, 0x07060302u)
+                              : __builtin_amdgcn_perm(vb2, va, 0x05040100u);
+          }
+          return as_h8(vb);
+        };
+        // A residual tile (a few per segment, not the hot loop) takes one
+        // arithmetic or the other, chosen before its PV step: a correction
+        // after the fp16 step would turn an infinite value into inf - inf.
+        if (__builtin_expect(wide, 0)) {  // fp32 P against the (exact) fp16 values
+#pragma unroll
+          for (int nt = 0; nt < CPL; ++nt) {
+            const half8_t vh = cols(nt);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) st.o[nt] = mfma32(ps.get(i), (float)vh[i], st.o[nt]);
+          }
+          // Sigma P into the sum columns; the column test is redone from an
+          // opaque lane id, not kept live
+          int ln = lane;
+          asm volatile("" : "+v"(ln));
+          const float one = sum_lane<HD>(ln & 15) ? 1.0f : 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) st.ob = mfma32(ps.get(i), one, st.ob);
+        } else {
+#pragma unroll
+          for (int nt = 0; nt < CPL; ++nt) st.o[nt] = mfma(prh, cols(nt), st.o[nt]);
+          const uint32_t one2 = sum_col ? 0x3C003C00u : 0u;  // Sigma P into the sum columns
+          st.ob = mfma(prh, as_h8(u32x4{one2, one2, one2, one2}), st.ob);
+        }
+        progress(kResidualUnits);
+      }
+
+      // ---- segment output: O directly, or a partial for the merge workgroups ----
+      // row sums: Sigma P of O row 4j + i sits in the sum column C1 of row
+      // block j; a sum lane takes its group's Sigma P z from its left neighbour
+      const bool whole = (t_beg == 0 && t_fin == T);
+      const int64_t piece = (int64_t)b * NKV + h + w;
+      float rowscale[4], zsum[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float li = __shfl(st.ob[i], 16 * j + C1, 64);
+        const float left = __shfl(st.ob[i], lane - 1, 64);
+        zsum[i] = sum_col ? left : st.ob[i];
+        rowscale[i] = whole ? 1.0f / fmaxf(li, 1.0e-30f) : 1.0f;
+      }
+      float* dst = whole ? a.out + (int64_t)b * a.out_stride + (int64_t)h * G * HD
+                         : a.ws_acc + piece * G * HD;
+      // the lane's output offset, computed here: hoisted out of the segment
+      // loop it would hold two registers for the whole run
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int lane_off = (ln >> 4) * 4 * HD + CPL * (ln & 15);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 4 * j + i;
+        if (row < G) {
+          float v[CPL];
+#pragma unroll
+          for (int nt = 0; nt < CPL; ++nt) v[nt] = (st.o[nt][i] + zsum[i]) * rowscale[i];
+          float* p = dst + lane_off + i * HD;
+          if (whole) {
+#pragma unroll
+            for (int q4 = 0; q4 < CPL / 4; ++q4)
+              *(floatx4*)(p + 4 * q4) =
+                  floatx4{v[4 * q4], v[4 * q4 + 1], v[4 * q4 + 2], v[4 * q4 + 3]};
+          } else if (CPL == 4) {  // read by a merge wavefront, possibly on another XCD
+            st_agent4(p, floatx4{v[0], v[1], v[2], v[3]});
+          } else {
+            // agent-scope stores bypass the L2, so each instruction should
+            // write whole sectors: lane c of the row's 16 takes floats
+            // 4c .. 4c + 3 and then 64 + 4c .. 64 + 4c + 3 (held by lanes c / 2
+            // and 8 + c / 2, half c % 2), two 256-byte contiguous stores
+            float* row_base = dst + (((ln >> 4) << 2) + i) * HD;
+            const int cl = ln & 15, src0 = (ln & 48) + (cl >> 1), hi = cl & 1;
+#pragma unroll
+            for (int part = 0; part < 2; ++part) {
+              const int src = src0 + 8 * part;
+              floatx4 o;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float lo_half = __shfl(v[e], src, 64), hi_half = __shfl(v[4 + e], src, 64);
+                o[e] = hi ? hi_half : lo_half;
+              }
+              st_agent4(row_base + 64 * part + 4 * cl, o);
+            }
           }
         }
       }
-    }
-    if (!whole) {
-      float lh[4];  // Sigma P of head c (rows 4 (c >> 2) + i)
+      if (!whole) {
+        float lh[4];  // Sigma P of head c (rows 4 (c >> 2) + i)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) lh[i] = __shfl(st.ob[i], 16 * (c >> 2) + C1, 64);
-      if (j == 0 && c < G) {
-        const int ci = c & 3;
-        st_agent(a.ws_ml + (piece * G + c) * 2, st.m,
-                 ci == 0 ? lh[0] : ci == 1 ? lh[1] : ci == 2 ? lh[2] : lh[3]);
+        for (int i = 0; i < 4; ++i) lh[i] = __shfl(st.ob[i], 16 * (c >> 2) + C1, 64);
+        if (j == 0 && c < G) {
+          const int ci = c & 3;
+          st_agent(a.ws_ml + (piece * G + c) * 2, st.m,
+                   ci == 0 ? lh[0] : ci == 1 ? lh[1] : ci == 2 ? lh[2] : lh[3]);
+        }
+        // only a run's first and last segments can be cut
+        (t_beg == 0 ? cut_last : cut_first) = piece;
       }
-      // only a run's first and last segments can be cut
-      (t_beg == 0 ? cut_last : cut_first) = piece;
-    }
-    // fused step: the wavefront that decoded the whole aging segment was its
-    // only reader; it clears the writer's flags (a cut one: its merge)
-    if constexpr (FUSED) {
-      if (ages && whole && lane == 0) {
-        uint64_t* f = a.ws_wflag + 2 * ((int64_t)b * NKV + h);
-        __hip_atomic_store(f, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(f + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // fused step: the wavefront that decoded the whole aging segment was its
+      // only reader; it clears the writer's flags (a cut one: its merge)
+      if constexpr (FUSED) {
+        if (ages && whole && lane < step_flags<HD>())
+          __hip_atomic_store(a.ws_wflag + step_flags<HD>() * ((int64_t)b * NKV + h) + lane, 0ull,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
+    if (x_rot < 0) break;
+    // the second pass: the rotated-away first segment
+    x = x_rot;
+    xe = x_rot_end;
+    sp = sp_rot;
+    kvh = kvh_rot;
+    u = u_rot;
+    x_rot = -1;
   }
   // flags after the run: the partials are complete at the point of coherence
   // before their flags are
@@ -1769,6 +1888,7 @@ __device__ __attribute__((always_inline)) inline uint64_t stream_run(
     if (cut_last >= 0)
       __hip_atomic_store(a.ws_flag + cut_last, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  if constexpr (FUSED) return t_wait;  // profiling: the wait, not t_first
   return t_first;
 }
 
@@ -1798,7 +1918,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   const int bid = (int)blockIdx.x - (FUSED ? a.writer_waves : 0);
   if constexpr (FUSED) {
     if (bid < 0) {
-      step_writer<HD>(g, a, (int)blockIdx.x, lane);
+      // top issue priority: the stream wavefronts start at 3 too, and a
+      // writer left below them ran for about 100 us while decode wavefronts
+      // waited for its age-outs
+      __builtin_amdgcn_s_setprio(3);
+      const uint64_t ph = step_writer<HD>(g, a, (int)blockIdx.x, lane);
+      write_stamp(a, t_start, (1ull << 62) | ph, lane);  // profiling: a writer wavefront
       return;
     }
   }
@@ -1875,6 +2000,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   const uint64_t t_first = stream_run<HD, P, PACK, FUSED>(
       g, a, ring, qrows, nb, sscale, lane, x0, x1, sp, one_pass, first_T, first_ov, first_n, w);
   // profiling: the run's units (bits 0-31) and the ticks to its first group (32-63)
+  if constexpr (FUSED) {  // profiling: the run's units and the ticks it waited for the writer
+    write_stamp(a, t_start, (uint64_t)(x1 - x0) | ((t_first & ((1ull << 30) - 1)) << 32), lane);
+    return;
+  }
   write_stamp(a, t_start, (uint64_t)(x1 - x0) | ((t_first ? t_first - t_start : 0) << 32), lane);
 }
 
