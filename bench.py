@@ -69,6 +69,9 @@ def parse():
     ap.add_argument("--wave-stamps", default="", metavar="NPY",
                     help="save per-workgroup start/end stamps of every timed decode of the "
                          "first pass to NPY (jacq_kivi_profile_wave_stamps)")
+    ap.add_argument("--stamp-pass", choices=("fused", "decode"), default="fused",
+                    help="which pass --wave-stamps records: the fused launches of the first "
+                         "pass, or the plain decode launches of the two-launch pass")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the workload, copy MIB MiB device-to-device a few times "
                          "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -202,7 +205,9 @@ def main() -> int:
             if not fused:
                 cache.append(nk[gi][:, None], nv[gi][:, None], bt, lens_before)
             e[1].record(stream)
-            if stamps is not None and not split and fused and i >= args.warmup:
+            stamp_this = (stamps is not None and not split and i >= args.warmup
+                          and fused == (args.stamp_pass == "fused"))
+            if stamp_this:
                 kivi.lib().jacq_kivi_profile_wave_stamps(
                     kivi._ptr(stamps[i - args.warmup]), STAMP_CAP)
             if fused:
@@ -210,7 +215,7 @@ def main() -> int:
                                    workspace=workspace)
             else:
                 cache.decode(qs[gi], lens_after, bt, out=out, workspace=workspace)
-            if stamps is not None:
+            if stamp_this:
                 kivi.lib().jacq_kivi_profile_wave_stamps(None, 0)
             e[2].record(stream)
             lens_before.add_(1)
@@ -237,10 +242,10 @@ def main() -> int:
         dec, _, _, host, wall = timed_pass(p1, split=False, fused=True)
     else:
         dec, _, _, host, wall = timed_pass(p1, split=False, fused=True)
-        if stamps is not None:
-            np.save(args.wave_stamps, stamps.cpu().numpy())
         kern, _, _, _, _ = timed_pass(p2, split=True, fused=True)
     sep_dec, _, sep_wr, _, _ = timed_pass(p3, split=False, fused=False)
+    if stamps is not None:
+        np.save(args.wave_stamps, stamps.cpu().numpy())
 
     def bytes_of(step0):
         return [geometry.decode_step_bytes(lens0 + step0 + i + 1, w.nh, w.nkv, w.hd, w.page,
