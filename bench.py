@@ -14,8 +14,8 @@ every step so the 256 MiB MALL and the L2 start cold.
 Prints ONE JSON line.  `value` is the effective KV bandwidth of the step
 (the decode's algorithmic bytes / step time, GB/s; the writer's few MB are not
 counted); the step time is the GPU time of the fused launch (one kernel: the
-writer wavefronts, the decode's stream wavefronts, then the workgroups that
-merge the split-K partials) from HIP events the library records on the launch
+decode's stream wavefronts, the first of which do the writer's work before
+their runs, then the workgroups that merge the split-K partials) from HIP events the library records on the launch
 stream before and after it (jacq_kivi_profile_*), and `ms_per_step` is that
 time per step.  `roofline.achieved` is the same bytes over the same time.
 A second pass of the same number of steps, continuing the token stream,

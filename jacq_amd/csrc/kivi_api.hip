@@ -346,8 +346,9 @@ void fill_ws(jacq::DecodeArgs& a, const KiviGeo& g, int batch, const SplitPlan& 
   a.ws_flag = ws ? (uint64_t*)(a.ws_acc + slots * g.hd) : nullptr;
 }
 
-// Fused write + decode: writer wavefronts at the front of the grid (about one
-// per 16 (sequence, kv head, K | V) pairs, at most 64), and one epoch flag per
+// Fused write + decode: the first stream wavefronts do the writer's work
+// before their (shorter) runs (about one per 8 (sequence, kv head, K | V)
+// pairs, at most 128), and one epoch flag per
 // age-out item (sequence, kv head, K | V, 32-channel slice) after the split-K
 // workspace.
 int step_writer_waves(const KiviGeo& g, int batch) {
@@ -424,7 +425,7 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
     max_tokens = ov + rv;
   }
   const int nw = step ? step_writer_waves(g, batch) : 0;
-  const int waves = jacq::decode_stream_waves(g, ds.cus) - nw;
+  const int waves = jacq::decode_stream_waves(g, ds.cus);  // writer wavefronts included
   const SplitPlan sp =
       per_query ? plan_splits_per_query(g, max_tokens, waves) : plan_splits(max_tokens);
   const size_t need = workspace_bytes(g, batch, sp, waves) + (step ? step_flag_bytes(g, batch) : 0);
@@ -700,8 +701,7 @@ size_t jacq_kivi_write_decode_workspace_size(const jacq_kivi_geometry* geo, int3
   int dev = 0;
   if (current_device(&dev) != JACQ_KIVI_OK) return 0;
   const KiviGeo g = make_geo(*geo);
-  const int waves = jacq::decode_stream_waves(g, device_state(dev).cus) -
-                    step_writer_waves(g, batch);
+  const int waves = jacq::decode_stream_waves(g, device_state(dev).cus);
   return workspace_bytes(g, batch, plan_splits(max_seq_len(*geo)), waves) +
          step_flag_bytes(g, batch);
 }

@@ -1026,12 +1026,26 @@ __device__ inline int64_t seq_start(const KiviGeo& g, const DecodeArgs& a, int b
   return run * g.nkv;
 }
 
-// First unit of wavefront w's run, and the wavefront whose run holds unit x.
-__device__ inline int64_t run_begin(int64_t w, int64_t TT, int64_t W) { return w * TT / W; }
-__device__ inline int64_t wave_of(int64_t x, int64_t TT, int64_t W) {
-  int64_t w = x * W / TT;
-  while (w > 0 && run_begin(w, TT, W) > x) --w;
-  while (w + 1 < W && run_begin(w + 1, TT, W) <= x) ++w;
+// Run weights, in sixteenths: a run of the fused step's writer wavefronts
+// (the first nw runs) weighs kWriterRun, every other run kRun, so the waves
+// that first do the writer's age-outs take shorter runs of the stream (by
+// per-wave stamps at 14B, a writer's items take about a quarter of a run).
+constexpr int kRun = 16, kWriterRun = 13;
+__device__ inline int64_t run_weight_sum(int64_t w, int64_t nw) {
+  return kRun * w - (kRun - kWriterRun) * (w < nw ? w : nw);
+}
+// First unit of wavefront w's run, and the wavefront whose run holds unit x
+// (W runs over TT units, the first nw of them writer runs).
+__device__ inline int64_t run_begin(int64_t w, int64_t TT, int64_t W, int64_t nw = 0) {
+  return TT * run_weight_sum(w, nw) / run_weight_sum(W, nw);
+}
+__device__ inline int64_t wave_of(int64_t x, int64_t TT, int64_t W, int64_t nw = 0) {
+  const int64_t c = x * run_weight_sum(W, nw) / TT;  // the weight sum at x, rounded down
+  const int64_t n = nw < W ? nw : W;
+  int64_t w = c < kWriterRun * n ? c / kWriterRun : n + (c - kWriterRun * n) / kRun;
+  if (w > W - 1) w = W - 1;
+  while (w > 0 && run_begin(w, TT, W, nw) > x) --w;
+  while (w + 1 < W && run_begin(w + 1, TT, W, nw) <= x) ++w;
   return w;
 }
 
@@ -1105,6 +1119,7 @@ __device__ __attribute__((always_inline)) inline void merge_segments(const KiviG
   // the whole call's stream (per-query split: each segment's own query, below)
   const int64_t TT = PQ ? 0 : stream_units(g, a, lane);
   const int64_t W = PQ ? 0 : stream_waves(TT, a.waves);
+  const int64_t nw = FUSED ? a.writer_waves : 0;  // writer runs (PQ: none)
   const int nseg = a.batch * NKV;
   const uint64_t epoch = a.epoch + a.merge_skew, t_start = __builtin_amdgcn_s_memrealtime();
   // wave-uniform: the wait ran out.  A merge of an earlier launch on this
@@ -1122,7 +1137,7 @@ __device__ __attribute__((always_inline)) inline void merge_segments(const KiviG
     gi[k] = 4 * e / HD;
     d[k] = 4 * e - gi[k] * HD;
   }
-  for (int seg = (int)blockIdx.x - a.writer_waves - a.waves; seg < nseg; seg += a.merge_wgs) {
+  for (int seg = (int)blockIdx.x - a.waves; seg < nseg; seg += a.merge_wgs) {
     const int b = seg / NKV, h = seg - b * NKV;
     int ov, n;
     const int T = seq_tiles(g, a, b, &ov, &n);
@@ -1140,10 +1155,11 @@ __device__ __attribute__((always_inline)) inline void merge_segments(const KiviG
       S0 = seq_start(g, a, b, lane) + (int64_t)h * units;
     }
     const int64_t S1 = S0 + units;
-    const int64_t w0 = wave_of(S0, sq, wq), w1 = wave_of(S1 - 1, sq, wq);
+    const int64_t w0 = wave_of(S0, sq, wq, nw), w1 = wave_of(S1 - 1, sq, wq, nw);
     // non-empty pieces: the runs that own at least one tile of the segment
     auto owns = [&](int64_t w) {
-      const int64_t x0 = max(run_begin(w, sq, wq), S0), x1 = min(run_begin(w + 1, sq, wq), S1);
+      const int64_t x0 = max(run_begin(w, sq, wq, nw), S0),
+                    x1 = min(run_begin(w + 1, sq, wq, nw), S1);
       return tile_at((int)(x0 - S0), nq) < tile_at((int)(x1 - S0), nq);
     };
     int pieces = 0;
@@ -1269,8 +1285,9 @@ __device__ __attribute__((always_inline)) inline void merge_segments(const KiviG
 //
 // jacq_kivi_write_decode appends one token per sequence (length seq_lens - 1
 // before, seq_lens after) and decodes the new state in one launch.  The
-// writer's work rides on a few wavefronts at the front of the grid, which are
-// dispatched before any decode wavefront and wait for nothing:
+// writer's work rides on the first stream wavefronts of the grid, which are
+// dispatched before the others, do it first (waiting for nothing) and then
+// decode a run of the stream shorter than the others' (kWriterRun):
 //  - a plain append stores the new token in scratch row r0.  No decode
 //    wavefront of this launch reads that row from the scratch: the residual
 //    tile that holds it takes the row from NEW_K / NEW_V instead;
@@ -1914,17 +1931,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
 
   const int lane = threadIdx.x;
   const uint64_t t_start = a.stamps ? __builtin_amdgcn_s_memrealtime() : 0;
-  // fused step: writer wavefronts first, then the stream, then the merges
-  const int bid = (int)blockIdx.x - (FUSED ? a.writer_waves : 0);
+  // the stream wavefronts (in the fused step the first writer_waves of them
+  // do the writer's work first), then the merges
+  const int bid = (int)blockIdx.x;
+  uint64_t writer_bit = 0;  // profiling: marks a writer wavefront's stamp
   if constexpr (FUSED) {
-    if (bid < 0) {
+    if (bid < a.writer_waves) {
       // top issue priority: the stream wavefronts start at 3 too, and a
       // writer left below them ran for about 100 us while decode wavefronts
       // waited for its age-outs
       __builtin_amdgcn_s_setprio(3);
-      const uint64_t ph = step_writer<HD>(g, a, (int)blockIdx.x, lane);
-      write_stamp(a, t_start, (1ull << 62) | ph, lane);  // profiling: a writer wavefront
-      return;
+      step_writer<HD>(g, a, bid, lane);
+      writer_bit = 1ull << 62;
     }
   }
   if (bid >= a.waves) {
@@ -1969,8 +1987,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
                               : stream_units(g, a, lane);
   const int64_t W = stream_waves(TT, a.waves);
   const int w = bid;
+  const int64_t nw = FUSED ? a.writer_waves : 0;
   if (w >= W) return;
-  const int64_t x0 = (int64_t)w * TT / W, x1 = (int64_t)(w + 1) * TT / W;
+  const int64_t x0 = run_begin(w, TT, W, nw), x1 = run_begin(w + 1, TT, W, nw);
   if (x0 >= x1) return;
 
   const Nibble nb;
@@ -2001,7 +2020,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
       g, a, ring, qrows, nb, sscale, lane, x0, x1, sp, one_pass, first_T, first_ov, first_n, w);
   // profiling: the run's units (bits 0-31) and the ticks to its first group (32-63)
   if constexpr (FUSED) {  // profiling: the run's units and the ticks it waited for the writer
-    write_stamp(a, t_start, (uint64_t)(x1 - x0) | ((t_first & ((1ull << 30) - 1)) << 32), lane);
+    write_stamp(a, t_start,
+                writer_bit | (uint64_t)(x1 - x0) | ((t_first & ((1ull << 30) - 1)) << 32), lane);
     return;
   }
   write_stamp(a, t_start, (uint64_t)(x1 - x0) | ((t_first ? t_first - t_start : 0) << 32), lane);
@@ -2010,7 +2030,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
 template <int HD, int P>
 static void launch_one(const KiviGeo& g, const DecodeArgs& a, hipStream_t stream,
                        hipEvent_t start, hipEvent_t stop) {
-  const dim3 grid(a.writer_waves + a.waves + a.merge_wgs);
+  const dim3 grid(a.waves + a.merge_wgs);
   const dim3 block(64);
   if (a.writer_waves > 0) {
     if (g.gqa <= 8)

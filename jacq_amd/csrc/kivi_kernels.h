@@ -61,7 +61,8 @@ struct DecodeArgs {
   int per_query = 0;  // matrix-core kernel: cut each query's streams by its own length alone
   // Fused write + decode (jacq_kivi_write_decode): the writer's arrays (one
   // new token per sequence; its length before the write is seq_lens - 1), the
-  // writer wavefronts at the front of the grid, and per (sequence, kv head,
+  // count of stream wavefronts at the front of the grid that do the writer's
+  // work before their runs, and per (sequence, kv head,
   // K | V) the epoch of the launch whose writer finished that age-out.
   AppendArgs wr{};
   uint64_t* ws_wflag = nullptr;

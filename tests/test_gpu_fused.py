@@ -96,7 +96,7 @@ def test_write_decode_every_sequence_ages_out(kivi, name):
 def test_write_decode_equals_append_then_decode(kivi):
     """The fused step leaves the same cache bits as jacq_kivi_cache_append
     followed by jacq_kivi_decode, and decodes to the same values within the
-    rounding of its own run split (its writer wavefronts take stream slots,
+    rounding of its own run split (its writer wavefronts take shorter runs,
     so the decode's cut differs)."""
     w = wl.WORKLOADS["qwen14b"].scaled(batch=8, ctx_lo=1000)
     lens = np.array([1000, 2207, 4095, 159, 160, 3000, 5000, 2048])
