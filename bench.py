@@ -315,7 +315,9 @@ def main() -> int:
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "wall_s_timed_region": round(wall, 4),
         "roofline": {
-            "kernel": "kivi_decode_stream_kernel<128, 16, true, false, true> (fused write + decode)",
+            "kernel": f"kivi_decode_stream_kernel<{w.hd}, {w.page}, "
+                      f"{'true' if w.nh // w.nkv <= 8 else 'false'}, false, true> "
+                      f"(fused write + decode)",
             "bound": "hbm",
             "achieved": round(gbs, 1),
             "peak": HBM_PEAK_GBS,

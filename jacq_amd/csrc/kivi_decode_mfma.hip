@@ -1111,8 +1111,9 @@ __device__ inline void write_stamp(const DecodeArgs& a, uint64_t t0, uint64_t in
 // The pieces of a segment are recomputed from the same split the stream
 // wavefronts used; a segment with a single non-empty piece was written whole.
 template <int HD, bool PACK, bool PQ, bool FUSED>
-__device__ __attribute__((always_inline)) inline void merge_segments(const KiviGeo& g,
-                                                                   const DecodeArgs& a, int lane) {
+__device__ __attribute__((always_inline)) inline uint64_t merge_segments(const KiviGeo& g,
+                                                                       const DecodeArgs& a,
+                                                                       int lane) {
   constexpr int K = (PACK ? 8 : 16) * HD / 256;  // float4 outputs per lane: G * HD <= 256 K
   constexpr int U = K <= 2 ? 8 : K > 4 ? 1 : 2;  // partials whose loads are in flight together
   const int G = g.gqa, NKV = g.nkv, n4 = G * HD / 4;
@@ -1128,6 +1129,7 @@ __device__ __attribute__((always_inline)) inline void merge_segments(const KiviG
   // repeats, so until the host resets the workspace every merged segment is
   // NaN and no flag is consumed.
   bool late = a.ws_poison && ld_agent(a.ws_poison) == kWorkspacePoison;
+  uint64_t t_land = t_start;  // profiling: when the last wait ended
   int gi[K], d[K];
   bool on[K];
 #pragma unroll
@@ -1195,6 +1197,7 @@ __device__ __attribute__((always_inline)) inline void merge_segments(const KiviG
         // ... then one round finds how many after it have landed too
         const uint64_t landed =
             __builtin_amdgcn_ballot_w64((todo & bit) && ld_agent(flag) == epoch);
+        if (a.stamps) t_land = __builtin_amdgcn_s_memrealtime();
         // the ready prefix: pieces of todo below its first one not yet stored
         const uint64_t waiting = todo & ~landed;
         uint64_t ready = waiting ? todo & ((waiting & (0 - waiting)) - 1) : todo;
@@ -1279,6 +1282,7 @@ __device__ __attribute__((always_inline)) inline void merge_segments(const KiviG
       __hip_atomic_store(a.ws_poison, kWorkspacePoison, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (a.status) __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
+  return t_land - t_start;
 }
 
 // ---- fused write + decode: the writer wavefronts ----
@@ -1292,13 +1296,14 @@ __device__ __attribute__((always_inline)) inline void merge_segments(const KiviG
 //    wavefront of this launch reads that row from the scratch: the residual
 //    tile that holds it takes the row from NEW_K / NEW_V instead;
 //  - a sequence that ages a group out (its 32 oldest scratch rows become int4
-//    pages) is one item per (kv head, K or V): quantise rows 0..31 into the
-//    group's pages, shift the scratch down 32 rows, store the new token in
-//    rows R - 1 and r0 (the writer's final state, stale copy included), then
-//    a release fence and the launch's epoch in the item's flag.  Decode
-//    wavefronts that read the new group or the residual tiles of such a
-//    segment wait for both of its flags (and acquire) before their first load
-//    of them; the wavefront or merge that finishes the segment clears them.
+//    pages) is one item per (kv head, K or V, 32-channel slice): quantise
+//    rows 0..31 into the group's pages, shift the scratch down 32 rows, store
+//    the new token in rows R - 1 and r0 (the writer's final state, stale copy
+//    included), all with device-scope stores, then wait for them and store
+//    the launch's epoch in the item's flag.  Decode wavefronts that read the
+//    new group or the residual tiles of such a segment wait for all of its
+//    flags before their first (device-scope) load of them; the wavefront or
+//    merge that finishes the segment clears them.
 // The arithmetic is the writer kernel's (kivi_append_kernel), so pages and
 // scratch end bit for bit as a separate write would leave them.
 
@@ -1946,8 +1951,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     }
   }
   if (bid >= a.waves) {
-    merge_segments<HD, PACK, PQ, FUSED>(g, a, lane);
-    write_stamp(a, t_start, 0, lane);
+    // profiling: the ticks from the merge's start to the end of its last wait
+    const uint64_t t_wait = merge_segments<HD, PACK, PQ, FUSED>(g, a, lane);
+    write_stamp(a, t_start, (t_wait & ((1ull << 30) - 1)) << 32, lane);
     return;
   }
   if constexpr (PQ) {
