@@ -278,38 +278,25 @@ def check_launch_device(tensors, op_name: str) -> None:
         raise KiviCheckError(f"{op_name}: {e}") from None
 
 
-def _check_supported_geometry(nh: int, nkv: int, name: str) -> None:
-    ok = (nh, nkv) in ((V1_NH, V1_NKV), (TP2_LOCAL_NH, TP2_LOCAL_NKV))
-    _check(ok, name, " supports global NH/NKV 40/8 or TP=2 local-rank NH/NKV 20/4; got NH=", nh,
-           " NKV=", nkv)
+def _validated(op: str, named, *args) -> None:
+    """The op's checks before a launch: GPU residency and contiguity of the
+    named tensors, then the op's fail-closed table -- run by the torch op's
+    ``<op>_check`` twin (csrc/kivi_torch_ops.cpp, the one copy of the table:
+    ranks, dtypes, shapes, geometry, lengths, table widths), its RuntimeError
+    raised as KiviCheckError -- then one device of the validated
+    architecture."""
+    from jacq_amd import torch_ops
+    for t, n in named:
+        check_cuda_tensor(t, n)
+    try:
+        getattr(torch_ops.load(), op + "_check")(*args)
+    except RuntimeError as e:
+        raise KiviCheckError(str(e).splitlines()[0]) from None
+    check_launch_device([t for t, _ in named], op)
 
 
-def _check_dtypes(pairs) -> None:
-    names = {torch.float16: "fp16", torch.int32: "int32", torch.uint8: "uint8",
-             torch.int64: "int64", torch.float32: "fp32"}
-    for t, dt, name in pairs:
-        _check(t.dtype == dt, name, " must be ", names[dt])
-
-
-def _check_pool(k_code, k_scale, k_zero, v_code, v_scale, v_zero, k_scr, v_scr, nkv):
-    nb = k_code.size(0)
-    _check(nb > 0, "K_CODE_PAGES dim 0 (page storage capacity) must be positive")
-    check_shape(k_code, (nb, nkv, BLOCK_SIZE, HD_PACKED), "K_CODE_PAGES")
-    check_shape(k_scale, (nb, nkv, V1_HD), "K_SCALE_PAGES")
-    check_shape(k_zero, (nb, nkv, V1_HD), "K_ZERO_PAGES")
-    check_shape(v_code, (nb, nkv, BLOCK_SIZE, HD_PACKED), "V_CODE_PAGES")
-    check_shape(v_scale, (nb, nkv, BLOCK_SIZE, HD_GROUPS), "V_SCALE_PAGES")
-    check_shape(v_zero, (nb, nkv, BLOCK_SIZE, HD_GROUPS), "V_ZERO_PAGES")
-    check_shape(k_scr, (nkv, RESIDUAL_SCRATCH, V1_HD), "K_RESIDUAL_SCRATCH")
-    check_shape(v_scr, (nkv, RESIDUAL_SCRATCH, V1_HD), "V_RESIDUAL_SCRATCH")
-
-
-def _pool_dtypes(k_code, k_scale, k_zero, v_code, v_scale, v_zero, k_scr, v_scr):
-    return [(k_code, torch.uint8, "K_CODE_PAGES"), (v_code, torch.uint8, "V_CODE_PAGES"),
-            (k_scale, torch.float16, "K_SCALE_PAGES"), (k_zero, torch.float16, "K_ZERO_PAGES"),
-            (v_scale, torch.float16, "V_SCALE_PAGES"), (v_zero, torch.float16, "V_ZERO_PAGES"),
-            (k_scr, torch.float16, "K_RESIDUAL_SCRATCH"),
-            (v_scr, torch.float16, "V_RESIDUAL_SCRATCH")]
+POOL_NAMES = ("K_CODE_PAGES", "K_SCALE_PAGES", "K_ZERO_PAGES", "V_CODE_PAGES", "V_SCALE_PAGES",
+              "V_ZERO_PAGES", "K_RESIDUAL_SCRATCH", "V_RESIDUAL_SCRATCH")
 
 
 # ---------------------------------------------------------------------------
@@ -322,24 +309,10 @@ def kivi_decode_dsl(q, block_table, k_code_pages, k_scale_pages, k_zero_pages, v
     """source_patch.py:768-869."""
     pool = (k_code_pages, k_scale_pages, k_zero_pages, v_code_pages, v_scale_pages, v_zero_pages,
             k_residual_scratch, v_residual_scratch)
-    names = ("K_CODE_PAGES", "K_SCALE_PAGES", "K_ZERO_PAGES", "V_CODE_PAGES", "V_SCALE_PAGES",
-             "V_ZERO_PAGES", "K_RESIDUAL_SCRATCH", "V_RESIDUAL_SCRATCH")
-    check_cuda_tensor(q, "Q")
-    check_cuda_tensor(block_table, "BLOCK_TABLE")
-    for t, n in zip(pool, names):
-        check_cuda_tensor(t, n)
-    check_cuda_tensor(out, "O")
-    _check_dtypes([(q, torch.float16, "Q"), (block_table, torch.int32, "BLOCK_TABLE")]
-                  + _pool_dtypes(*pool) + [(out, torch.float32, "O")])
-    _check(k_code_pages.dim() >= 2, "K_CODE_PAGES must expose NKV at dim 1")
-    nh, nkv = q.size(0), k_code_pages.size(1)
-    _check_supported_geometry(nh, nkv, "kivi_decode_dsl")
-    check_shape(q, (nh, V1_HD), "Q")
-    check_block_table_width(block_table, "BLOCK_TABLE", seq_len)
-    _check_pool(*pool, nkv)
-    check_shape(out, (nh, V1_HD), "O")
-    check_launch_device([q, block_table, *pool, out], "kivi_decode_dsl")
-    fn = lib().jac_launch_tp2_local if nh == TP2_LOCAL_NH else lib().jac_launch
+    _validated("kivi_decode_dsl",
+               [(q, "Q"), (block_table, "BLOCK_TABLE"), *zip(pool, POOL_NAMES), (out, "O")],
+               q, block_table, *pool, int(seq_len), out)
+    fn = lib().jac_launch_tp2_local if q.size(0) == TP2_LOCAL_NH else lib().jac_launch
     fn(_ptr(q), _ptr(block_table), *[_ptr(t) for t in pool], int(seq_len), _ptr(out),
        _stream(q.device))
 
@@ -352,32 +325,11 @@ def kivi_decode_sparse_retained_dsl(q, retained_block_table, k_code_pages, k_sca
     entries of a compact retained-page table, residual at the dense SEQ_LEN."""
     pool = (k_code_pages, k_scale_pages, k_zero_pages, v_code_pages, v_scale_pages, v_zero_pages,
             k_residual_scratch, v_residual_scratch)
-    names = ("K_CODE_PAGES", "K_SCALE_PAGES", "K_ZERO_PAGES", "V_CODE_PAGES", "V_SCALE_PAGES",
-             "V_ZERO_PAGES", "K_RESIDUAL_SCRATCH", "V_RESIDUAL_SCRATCH")
-    check_cuda_tensor(q, "Q")
-    check_cuda_tensor(retained_block_table, "RETAINED_BLOCK_TABLE")
-    for t, n in zip(pool, names):
-        check_cuda_tensor(t, n)
-    check_cuda_tensor(out, "O")
-    _check_dtypes([(q, torch.float16, "Q"),
-                   (retained_block_table, torch.int32, "RETAINED_BLOCK_TABLE")]
-                  + _pool_dtypes(*pool) + [(out, torch.float32, "O")])
-    _check(k_code_pages.dim() >= 2, "K_CODE_PAGES must expose NKV at dim 1")
-    nh, nkv = q.size(0), k_code_pages.size(1)
-    real_num_blocks = k_code_pages.size(0)
-    _check_supported_geometry(nh, nkv, "kivi_decode_sparse_retained_dsl")
-    _check(real_num_blocks > 0, "K_CODE_PAGES dim 0 (page storage capacity) must be positive")
-    check_shape(q, (nh, V1_HD), "Q")
-    check_shape(retained_block_table, (OLD_BLOCKS,), "RETAINED_BLOCK_TABLE")
-    _check_pool(*pool, nkv)
-    check_shape(out, (nh, V1_HD), "O")
-    _check(1 <= seq_len <= OLD_BLOCKS * BLOCK_SIZE + RESIDUAL,
-           "SEQ_LEN must be in [1, 4096] for Qwen2.5-Coder-32B KIVI sparse-retained DSL ABI")
-    _check(0 <= num_retained_pages <= OLD_BLOCKS, "NUM_RETAINED_PAGES must be in [0, OLD_BLOCKS]")
-    _check(num_retained_pages <= real_num_blocks,
-           "NUM_RETAINED_PAGES cannot exceed physical page storage capacity")
-    check_launch_device([q, retained_block_table, *pool, out], "kivi_decode_sparse_retained_dsl")
-    fn = (lib().jac_launch_sparse_retained_tp2_local if nh == TP2_LOCAL_NH
+    _validated("kivi_decode_sparse_retained_dsl",
+               [(q, "Q"), (retained_block_table, "RETAINED_BLOCK_TABLE"),
+                *zip(pool, POOL_NAMES), (out, "O")],
+               q, retained_block_table, *pool, int(seq_len), int(num_retained_pages), out)
+    fn = (lib().jac_launch_sparse_retained_tp2_local if q.size(0) == TP2_LOCAL_NH
           else lib().jac_launch_sparse_retained)
     fn(_ptr(q), _ptr(retained_block_table), *[_ptr(t) for t in pool], int(seq_len),
        int(num_retained_pages), _ptr(out), _stream(q.device))
@@ -389,60 +341,18 @@ def kivi_decode_batched_dsl(q, seq_lens, block_table, k_code_pages, k_scale_page
     """source_patch.py:1268-1386 (one sequence, up to 160 causal queries)."""
     pool = (k_code_pages, k_scale_pages, k_zero_pages, v_code_pages, v_scale_pages, v_zero_pages,
             k_residual_scratch, v_residual_scratch)
-    for t, n in [(q, "Q"), (seq_lens, "SEQ_LENS"), (block_table, "BLOCK_TABLE"), (out, "O")]:
-        check_cuda_tensor(t, n)
-    for t in pool:
-        check_cuda_tensor(t, "KIVI cache tensor")
-    _check_dtypes([(q, torch.float16, "Q"), (seq_lens, torch.int32, "SEQ_LENS"),
-                   (block_table, torch.int32, "BLOCK_TABLE")] + _pool_dtypes(*pool)
-                  + [(out, torch.float32, "O")])
-    _check(q.dim() == 3, "Q rank mismatch for the batched KIVI DSL decode ABI")
-    nh, nkv = q.size(1), k_code_pages.size(1)
-    _check_supported_geometry(nh, nkv, "kivi_decode_batched_dsl")
-    _check(1 <= num_queries <= MAX_QUERIES,
-           "NUM_QUERIES must be in [1, MAX_QUERIES] for the batched KIVI DSL decode ABI")
-    check_shape(q, (num_queries, nh, V1_HD), "Q")
-    check_shape(seq_lens, (num_queries,), "SEQ_LENS")
-    _check_pool(*pool, nkv)
-    check_shape(out, (num_queries, nh, V1_HD), "O")
-    for i, s in enumerate(seq_lens.cpu().tolist()):  # source_patch.py:1352-1360
-        _check(1 <= s <= OLD_BLOCKS * BLOCK_SIZE + RESIDUAL, "SEQ_LENS[", i,
-               "] must be in [1, 4096] for the batched KIVI DSL decode ABI, got ", s)
-        check_block_table_width(block_table, "BLOCK_TABLE", s)
-    check_launch_device([q, seq_lens, block_table, *pool, out], "kivi_decode_batched_dsl")
-    fn = lib().jac_launch_batched_tp2_local if nh == TP2_LOCAL_NH else lib().jac_launch_batched
+    _validated("kivi_decode_batched_dsl",
+               [(q, "Q"), (seq_lens, "SEQ_LENS"), (block_table, "BLOCK_TABLE"),
+                *[(t, "KIVI cache tensor") for t in pool], (out, "O")],
+               q, seq_lens, block_table, *pool, int(num_queries), out)
+    fn = lib().jac_launch_batched_tp2_local if q.size(1) == TP2_LOCAL_NH else lib().jac_launch_batched
     fn(_ptr(q), _ptr(seq_lens), _ptr(block_table), *[_ptr(t) for t in pool], int(num_queries),
        _ptr(out), _stream(q.device))
 
 
-def _writer_checks(op, pool, new_k, new_v, slot_mapping, block_table, seq_len_end, num_new,
-                   nkv_fixed=None):
-    for t, n in [(new_k, "NEW_K"), (new_v, "NEW_V"), (slot_mapping, "SLOT_MAPPING"),
-                 (block_table, "BLOCK_TABLE")]:
-        check_cuda_tensor(t, n)
-    for t in pool:
-        check_cuda_tensor(t, "KIVI cache tensor")
-    _check_dtypes(_pool_dtypes(*pool) + [(new_k, torch.float16, "NEW_K"),
-                                         (new_v, torch.float16, "NEW_V"),
-                                         (slot_mapping, torch.int64, "SLOT_MAPPING"),
-                                         (block_table, torch.int32, "BLOCK_TABLE")])
-    nkv = pool[0].size(1) if nkv_fixed is None else nkv_fixed
-    if nkv_fixed is None:
-        _check_supported_geometry(V1_NH if nkv == V1_NKV else TP2_LOCAL_NH, nkv, op)
-    _check_pool(*pool, nkv)
-    if num_new is None:
-        check_shape(new_k, (nkv, V1_HD), "NEW_K")
-        check_shape(new_v, (nkv, V1_HD), "NEW_V")
-        _check(slot_mapping.numel() == 1,
-               "SLOT_MAPPING must contain exactly one decode token in the first KIVI DSL writer lane")
-    else:
-        check_shape(new_k, (num_new, nkv, V1_HD), "NEW_K")
-        check_shape(new_v, (num_new, nkv, V1_HD), "NEW_V")
-        _check(slot_mapping.numel() == num_new,
-               "SLOT_MAPPING must contain exactly NUM_NEW entries for the batched KIVI DSL writer")
-    check_block_table_width(block_table, "BLOCK_TABLE", seq_len_end)
-    check_launch_device([*pool, new_k, new_v, slot_mapping, block_table], op)
-    return nkv
+def _writer_named(pool, new_k, new_v, slot_mapping, block_table):
+    return [*[(t, "KIVI cache tensor") for t in pool], (new_k, "NEW_K"), (new_v, "NEW_V"),
+            (slot_mapping, "SLOT_MAPPING"), (block_table, "BLOCK_TABLE")]
 
 
 def kivi_cache_write_dsl(k_code_pages, k_scale_pages, k_zero_pages, v_code_pages, v_scale_pages,
@@ -451,13 +361,11 @@ def kivi_cache_write_dsl(k_code_pages, k_scale_pages, k_zero_pages, v_code_pages
     """source_patch.py:975-1078 -> kivi_cache_write_launch."""
     pool = (k_code_pages, k_scale_pages, k_zero_pages, v_code_pages, v_scale_pages, v_zero_pages,
             k_residual_scratch, v_residual_scratch)
-    _check(1 <= seq_len <= OLD_BLOCKS * BLOCK_SIZE + RESIDUAL,
-           "SEQ_LEN must be in [1, 4096] for the first KIVI DSL writer lane")
-    nkv = _writer_checks("kivi_cache_write_dsl", pool, new_k, new_v, slot_mapping, block_table,
-                         seq_len, None)
+    _validated("kivi_cache_write_dsl", _writer_named(pool, new_k, new_v, slot_mapping, block_table),
+               *pool, new_k, new_v, slot_mapping, block_table, int(seq_len))
     lib().kivi_cache_write_launch(*[_ptr(t) for t in pool], _ptr(new_k), _ptr(new_v),
-                                  _ptr(slot_mapping), _ptr(block_table), int(seq_len), int(nkv),
-                                  _stream(new_k.device))
+                                  _ptr(slot_mapping), _ptr(block_table), int(seq_len),
+                                  int(k_code_pages.size(1)), _stream(new_k.device))
 
 
 def kivi_cache_write_jac_dsl(k_code_pages, k_scale_pages, k_zero_pages, v_code_pages,
@@ -466,10 +374,9 @@ def kivi_cache_write_jac_dsl(k_code_pages, k_scale_pages, k_zero_pages, v_code_p
     """source_patch.py:1085-1180 -> jac_launch_cache_write (global geometry only)."""
     pool = (k_code_pages, k_scale_pages, k_zero_pages, v_code_pages, v_scale_pages, v_zero_pages,
             k_residual_scratch, v_residual_scratch)
-    _check(1 <= seq_len <= OLD_BLOCKS * BLOCK_SIZE + RESIDUAL,
-           "SEQ_LEN must be in [1, 4096] for the first KIVI DSL writer lane")
-    _writer_checks("kivi_cache_write_jac_dsl", pool, new_k, new_v, slot_mapping, block_table,
-                   seq_len, None, nkv_fixed=V1_NKV)
+    _validated("kivi_cache_write_jac_dsl",
+               _writer_named(pool, new_k, new_v, slot_mapping, block_table),
+               *pool, new_k, new_v, slot_mapping, block_table, int(seq_len))
     lib().jac_launch_cache_write(*[_ptr(t) for t in pool], _ptr(new_k), _ptr(new_v),
                                  _ptr(block_table), int(seq_len), _stream(new_k.device))
 
@@ -481,17 +388,13 @@ def kivi_cache_write_batched_dsl(k_code_pages, k_scale_pages, k_zero_pages, v_co
     """source_patch.py:1392-1495 -> kivi_cache_write_batched_launch."""
     pool = (k_code_pages, k_scale_pages, k_zero_pages, v_code_pages, v_scale_pages, v_zero_pages,
             k_residual_scratch, v_residual_scratch)
-    _check(1 <= num_new <= RESIDUAL_SCRATCH,
-           "NUM_NEW must be in [1, RESIDUAL_SCRATCH] -- callers must pre-split a prefill chunk "
-           "into sub-chunks via plan_batched_write before calling this op")
-    _check(start_seq_len >= 0 and start_seq_len + num_new <= OLD_BLOCKS * BLOCK_SIZE + RESIDUAL,
-           "START_SEQ_LEN + NUM_NEW must be in [0, 4096] for the batched KIVI DSL writer lane")
-    nkv = _writer_checks("kivi_cache_write_batched_dsl", pool, new_k, new_v, slot_mapping,
-                         block_table, start_seq_len + num_new, num_new)
+    _validated("kivi_cache_write_batched_dsl",
+               _writer_named(pool, new_k, new_v, slot_mapping, block_table),
+               *pool, new_k, new_v, slot_mapping, block_table, int(start_seq_len), int(num_new))
     lib().kivi_cache_write_batched_launch(*[_ptr(t) for t in pool], _ptr(new_k), _ptr(new_v),
                                           _ptr(slot_mapping), _ptr(block_table),
-                                          int(start_seq_len), int(num_new), int(nkv),
-                                          _stream(new_k.device))
+                                          int(start_seq_len), int(num_new),
+                                          int(k_code_pages.size(1)), _stream(new_k.device))
 
 
 def plan_batched_write(start_seq_len: int, num_new_tokens: int, residual: int = 128,

@@ -305,3 +305,22 @@ def test_random_serving_trace_keeps_slots_unique_and_stable():
             live[r] = x
         held = [v for v in live.values() if v >= 0]
         assert len(set(held)) == len(held), step
+
+
+@pytest.mark.parametrize("name,change,text", REJECT[::3],
+                         ids=[f"{i}-{r[0][5:]}" for i, r in enumerate(REJECT[::3])])
+def test_python_mirrors_use_the_same_table(name, change, text):
+    """jacq_amd.kivi's op mirrors validate through the ops' ``_check`` twins
+    (kivi._validated), so they refuse what the ops refuse, with the same text,
+    as KiviCheckError."""
+    from jacq_amd import kivi
+
+    class Mirror:
+        def __getattr__(self, attr):
+            return lambda *args: kivi._validated(attr[:-len("_check")], [], *args)
+
+    a = _args(name)
+    a.update(change)
+    with pytest.raises(kivi.KiviCheckError) as e:
+        _call(Mirror(), name, a)
+    assert text in str(e.value), str(e.value)
