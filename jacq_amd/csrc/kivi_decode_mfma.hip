@@ -1130,6 +1130,7 @@ __device__ __attribute__((always_inline)) inline uint64_t merge_segments(const K
   // NaN and no flag is consumed.
   bool late = a.ws_poison && ld_agent(a.ws_poison) == kWorkspacePoison;
   uint64_t t_land = t_start;  // profiling: when the last wait ended
+  uint32_t rounds_after = 0;  // profiling: load rounds after it
   int gi[K], d[K];
   bool on[K];
 #pragma unroll
@@ -1197,7 +1198,10 @@ __device__ __attribute__((always_inline)) inline uint64_t merge_segments(const K
         // ... then one round finds how many after it have landed too
         const uint64_t landed =
             __builtin_amdgcn_ballot_w64((todo & bit) && ld_agent(flag) == epoch);
-        if (a.stamps) t_land = __builtin_amdgcn_s_memrealtime();
+        if (a.stamps) {
+          t_land = __builtin_amdgcn_s_memrealtime();
+          rounds_after = 0;
+        }
         // the ready prefix: pieces of todo below its first one not yet stored
         const uint64_t waiting = todo & ~landed;
         uint64_t ready = waiting ? todo & ((waiting & (0 - waiting)) - 1) : todo;
@@ -1218,6 +1222,7 @@ __device__ __attribute__((always_inline)) inline uint64_t merge_segments(const K
             }
           }
           consumed &= ~ready;
+          ++rounds_after;
           uint64_t ml[U][K];
           floatx4 vv[U][K];
 #pragma unroll
@@ -1282,7 +1287,7 @@ __device__ __attribute__((always_inline)) inline uint64_t merge_segments(const K
       __hip_atomic_store(a.ws_poison, kWorkspacePoison, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (a.status) __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
-  return t_land - t_start;
+  return ((t_land - t_start) & ((1ull << 24) - 1)) | ((uint64_t)(rounds_after & 63) << 24);
 }
 
 // ---- fused write + decode: the writer wavefronts ----
@@ -1952,8 +1957,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   }
   if (bid >= a.waves) {
     // profiling: the ticks from the merge's start to the end of its last wait
+    // (bits 32-55) and the load rounds after that wait (bits 56-61)
     const uint64_t t_wait = merge_segments<HD, PACK, PQ, FUSED>(g, a, lane);
-    write_stamp(a, t_start, (t_wait & ((1ull << 30) - 1)) << 32, lane);
+    write_stamp(a, t_start, t_wait << 32, lane);
     return;
   }
   if constexpr (PQ) {

@@ -176,3 +176,28 @@ def test_write_decode_graph_replays(kivi):
         for x, y in zip(graphed.pool(), eager.pool()):
             assert torch.equal(x.view(torch.uint8), y.view(torch.uint8)), f"cache after replay {step}"
         cur += 1
+
+
+FUSED_GEOMETRIES = {
+    # page 32 at the v1 shape (GQA 5, the packed HD-128 kernel)
+    "v1_p32": wl.Workload("fv1", 40, 8, 128, 5, 160, 160, page=32, residual=128, outliers=8,
+                          outlier_scale=10.0, seed=61),
+    # HD 64 with GQA 10 (the unpacked kernel), page 32
+    "hd64_g10_p32": wl.Workload("f64", 40, 4, 64, 5, 160, 160, page=32, residual=128,
+                                outliers=4, outlier_scale=8.0, seed=62),
+    # HD 128 with GQA 16 (unpacked), page 16, and a 64-token residual window
+    "hd128_g16_r64": wl.Workload("f128", 32, 2, 128, 5, 96, 96, page=16, residual=64,
+                                 outliers=4, outlier_scale=8.0, seed=63),
+}
+
+
+@pytest.mark.parametrize("name", list(FUSED_GEOMETRIES))
+def test_write_decode_other_geometries(kivi, name):
+    """The fused step on the other kernel instantiations (page 32, HD 64,
+    GQA above 8 -- the unpacked kernels -- and another residual window):
+    bit-exact cache and in-tolerance decode over steps that cross age-outs."""
+    w = FUSED_GEOMETRIES[name]
+    R = w.residual
+    lens = [R + 31, R + 30 + 32 * 3, R + 1, R + 17 + 32 * 40, 2]
+    aged = _run_steps(kivi, w, lens, steps=34, seed=64, check_every=3)
+    assert aged >= 3
