@@ -424,8 +424,9 @@ int run_decode(const jacq_kivi_geometry& x, const jacq_half_t* Q, const int32_t*
     jacq::window_of(g, retained_pages, seq_len_host, &ov, &rv);
     max_tokens = ov + rv;
   }
-  const int nw = step ? step_writer_waves(g, batch) : 0;
   const int waves = jacq::decode_stream_waves(g, ds.cus);  // writer wavefronts included
+  // the writer wavefronts are stream wavefronts: never more than the grid holds
+  const int nw = step ? std::min(step_writer_waves(g, batch), waves) : 0;
   const SplitPlan sp =
       per_query ? plan_splits_per_query(g, max_tokens, waves) : plan_splits(max_tokens);
   const size_t need = workspace_bytes(g, batch, sp, waves) + (step ? step_flag_bytes(g, batch) : 0);
