@@ -7,7 +7,7 @@ A step is one pass of the hot path over the batch, in one launch
 sequence (aging out 32-token groups where a sequence crosses the residual
 window), then paged decode attention runs for one query token per sequence
 over the new state.  Inputs are synthetic (seeded N(0,1) with outlier K
-channels, BASELINE workload definitions in jacq_amd/workloads.py) and resident
+channels, the workload definitions in jacq_amd/workloads.py) and resident
 in HBM before timing starts.  A 512 MiB buffer is read (by default) before
 every step so the 256 MiB MALL and the L2 start cold.
 
@@ -312,6 +312,10 @@ def main() -> int:
             "decode_only_frac": round(sep_gbs / HBM_PEAK_GBS, 4),
         },
         "decode_bytes_per_step": int(bytes_per_step),
+        # the writer's share of the step, not in `value` (new rows, age-outs, shifts)
+        "writer_bytes_per_step": int(np.mean([
+            geometry.write_step_bytes(lens0 + p1 + i, w.nkv, w.hd, w.residual, w.group)
+            for i in range(args.warmup, total_steps)])),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "wall_s_timed_region": round(wall, 4),
         "roofline": {

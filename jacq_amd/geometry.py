@@ -200,3 +200,25 @@ def decode_step_bytes(seq_lens, num_heads: int, num_kv_heads: int, head_dim: int
         total += 4 * (old // page_size)
     total += len(seq_lens) * num_heads * head_dim * (2 + 4)
     return int(round(total))
+
+
+def write_step_bytes(lens_before, num_kv_heads: int, head_dim: int, residual: int,
+                     group_size: int = 32) -> int:
+    """HBM bytes of one one-token write per sequence (the fused step's writer
+    share, reported apart from the decode's bytes): the new K and V rows
+    (fp16), and for a sequence whose group ages out, the group's 32 rows read,
+    their codes and scale/zero pairs written, and the shift (the residual rows
+    read and written again) -- per kv head."""
+    g = LaneGeometry(num_kv_heads * 1, num_kv_heads, head_dim, 16, group_size, residual)
+    total = 0
+    for n in lens_before:
+        n = int(n)
+        total += num_kv_heads * 2 * head_dim * 2  # the new K and V rows
+        if g.old_tokens(n + 1) > g.old_tokens(n):
+            rows_in = 2 * group_size * head_dim * 2             # K and V rows of the group
+            codes = 2 * group_size * head_dim // 2              # K and V int4 codes
+            k_pairs = head_dim * PARAM_PAIR_BYTES               # per-channel K scale/zero
+            v_pairs = group_size * (head_dim // group_size) * PARAM_PAIR_BYTES
+            shift = 2 * 2 * residual * head_dim * 2             # K and V rows, read + write
+            total += num_kv_heads * (rows_in + codes + k_pairs + v_pairs + shift)
+    return total

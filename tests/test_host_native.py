@@ -212,6 +212,16 @@ def test_decode_bytes_formula():
     assert n == 8 * (3968 * 160 + 128 * 512) + 4 * 124 + 40 * 128 * 6
 
 
+def test_write_step_bytes_formula():
+    """The fused step's writer bytes: the new K and
+    V rows per sequence, and per age-out 2*32*HD*2 rows in, codes, the K and V
+    scale/zero pairs and the R-row shift read and written, per kv head."""
+    assert geometry.write_step_bytes([1000, 3000], 8, 128, 128) == 2 * 8 * 512  # no age-out
+    per_head = 2 * 32 * 128 * 2 + 2 * 32 * 64 + 128 * 4 + 32 * 4 * 4 + 2 * 2 * 128 * 256
+    # 159 -> 160 and 191 -> 192 age a group out, 160 -> 161 does not
+    assert geometry.write_step_bytes([159, 160, 191], 8, 128, 128) == 3 * 8 * 512 + 2 * 8 * per_head
+
+
 def plan_count_closed_form(start, num, residual, group):
     """Sub-chunks of the greedy plan (source_patch.py:521-546), from the
     arithmetic alone: the first takes the room left in the scratch,

@@ -65,7 +65,7 @@ def test_random_groups_equal_numpy_restatement(seed):
     scale = [1.0, 10.0, 1e-3, 300.0, 1.0, 0.05][seed]
     k = nq._bits(rng.standard_normal((32, 2, 128)) * scale)
     v = nq._bits(rng.standard_normal((32, 2, 128)) * scale)
-    if seed == 4:  # outlier channels (the BASELINE K recipe)
+    if seed == 4:  # outlier channels (the benchmark K recipe)
         k[:, :, ::16] = nq._bits(nq.f16(k[:, :, ::16]).astype(np.float32) * 10)
     assert_same(oracle_group(k, v), nq.quantise_group(k, v), f"seed {seed}")
 
