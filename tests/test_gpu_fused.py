@@ -201,3 +201,65 @@ def test_write_decode_other_geometries(kivi, name):
     lens = [R + 31, R + 30 + 32 * 3, R + 1, R + 17 + 32 * 40, 2]
     aged = _run_steps(kivi, w, lens, steps=34, seed=64, check_every=3)
     assert aged >= 3
+
+
+def test_write_decode_merge_timeout_is_reported(kivi):
+    """Failure handling in the fused step, forced from the host (the merge
+    waits for a tag nobody stores and gives up after 20 us): the launch ends,
+    the writer's work is complete and bit-exact (it waits for nothing), whole
+    segments decode correctly and merged ones are NaN; the next fused step is
+    refused without launching (cache and output untouched) until
+    jacq_kivi_decode_status resets, after which the step is correct again."""
+    from tests.test_gpu_parity import _segment_counts
+
+    w = wl.WORKLOADS["qwen14b"]
+    lens = np.array([3000, 159, 20, 700, 1])
+    st = State(w, lens=lens, extra_tokens=2, seed=71)
+    st.build_oracle()
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, st.max_pages,
+                            st.num_pages)
+    cache = kivi.PagedKiviCache.from_tensors(geo, to_torch(st))
+    bt = torch.from_numpy(st.tables).cuda()
+    q = torch.from_numpy(st.q).view(torch.float16).cuda()
+
+    def token(i):
+        nk = torch.stack([torch.from_numpy(st.k_hist[b][int(lens[b]) + i].copy())
+                          for b in range(st.batch)]).view(torch.float16).cuda()
+        nv = torch.stack([torch.from_numpy(st.v_hist[b][int(lens[b]) + i].copy())
+                          for b in range(st.batch)]).view(torch.float16).cuda()
+        return nk, nv
+
+    def oracle_step(i):
+        for b in range(st.batch):
+            o.cache_write(st.cache, b, st.k_hist[b][int(lens[b]) + i],
+                          st.v_hist[b][int(lens[b]) + i], st.tables[b], int(lens[b]) + i + 1)
+
+    kivi.decode_status()  # nothing pending
+    nk, nv = token(0)
+    after = torch.from_numpy((lens + 1).astype(np.int32)).cuda()
+    kivi.lib().jacq_kivi_test_force_merge_timeout(20)
+    try:
+        out = cache.write_decode(q, nk, nv, after, bt)
+        torch.cuda.synchronize()
+    finally:
+        kivi.lib().jacq_kivi_test_force_merge_timeout(0)
+    oracle_step(0)
+    _compare_all(st, cache, "after the timed-out step")
+    counts = _segment_counts(w, out.cpu().numpy().astype(np.float64), st.decode_ref(lens + 1))
+    assert counts["other"] == 0 and counts["nan"] >= 1 and counts["match"] >= 1, counts
+    # refused: nothing launched, the cache keeps the state of the step above
+    nk, nv = token(1)
+    after2 = torch.from_numpy((lens + 2).astype(np.int32)).cuda()
+    sentinel = torch.full_like(out, 7.0)
+    with pytest.raises(kivi.KiviMergeTimeout, match="timed out"):
+        cache.write_decode(q, nk, nv, after2, bt, out=sentinel)
+    torch.cuda.synchronize()
+    assert bool((sentinel == 7.0).all()), "a refused step must not launch"
+    _compare_all(st, cache, "after the refused step")
+    with pytest.raises(kivi.KiviMergeTimeout, match="reset"):
+        kivi.decode_status()
+    out = cache.write_decode(q, nk, nv, after2, bt)
+    torch.cuda.synchronize()
+    oracle_step(1)
+    _compare_all(st, cache, "after the reset")
+    assert_close(out.cpu().numpy(), st.decode_ref(lens + 2), "fused step after the reset")
