@@ -814,10 +814,14 @@ __device__ inline int64_t stream_units(const KiviGeo& g, const DecodeArgs& a, in
 // kMinUnitsPerWave units each, so that small batches spread over enough
 // wavefronts to hide the per-group latency chain without cutting every
 // segment into pieces the merge must fold (4: TinyLlama 17.9 -> 15.6 us,
-// Qwen0.5B 19.6 -> 18.5 us against 8; 2 was slower at Qwen0.5B).
-constexpr int kMinUnitsPerWave = 4;
-__device__ inline int64_t stream_waves(int64_t units, int grid) {
-  int64_t w = (units + kMinUnitsPerWave - 1) / kMinUnitsPerWave;
+// Qwen0.5B 19.6 -> 18.5 us against 8; 2 was slower at Qwen0.5B).  A whole
+// call's stream of fewer than kTinyStream units (TinyLlama's 72) takes 2 per
+// wavefront (0.9 us faster there; 1 was slower).  The per-query split keeps
+// 4: the host sizes its partial slots from that.
+constexpr int kMinUnitsPerWave = 4, kTinyStream = 256;
+__device__ inline int64_t stream_waves(int64_t units, int grid, bool whole_call = false) {
+  const int per = whole_call && units < kTinyStream ? 2 : kMinUnitsPerWave;
+  int64_t w = (units + per - 1) / per;
   if (w < 1) w = 1;
   return w < grid ? w : grid;
 }
@@ -1119,7 +1123,7 @@ __device__ __attribute__((always_inline)) inline uint64_t merge_segments(const K
   const int G = g.gqa, NKV = g.nkv, n4 = G * HD / 4;
   // the whole call's stream (per-query split: each segment's own query, below)
   const int64_t TT = PQ ? 0 : stream_units(g, a, lane);
-  const int64_t W = PQ ? 0 : stream_waves(TT, a.waves);
+  const int64_t W = PQ ? 0 : stream_waves(TT, a.waves, true);
   const int64_t nw = FUSED ? a.writer_waves : 0;  // writer runs (PQ: none)
   const int nseg = a.batch * NKV;
   const uint64_t epoch = a.epoch + a.merge_skew, t_start = __builtin_amdgcn_s_memrealtime();
@@ -1997,7 +2001,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   const int lane_incl = wave_incl_scan(lane_U, lane);
   const int64_t TT = one_pass ? (int64_t)NKV * __builtin_amdgcn_readlane(lane_incl, 63)
                               : stream_units(g, a, lane);
-  const int64_t W = stream_waves(TT, a.waves);
+  const int64_t W = stream_waves(TT, a.waves, true);
   const int w = bid;
   const int64_t nw = FUSED ? a.writer_waves : 0;
   if (w >= W) return;
