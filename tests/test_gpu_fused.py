@@ -12,7 +12,7 @@ import pytest
 
 from jacq_amd import workloads as wl
 from oracle import oracle as o
-from tests.kivi_testlib import State, assert_close, to_torch
+from tests.kivi_testlib import State, assert_close, geometry, to_torch
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -263,3 +263,40 @@ def test_write_decode_merge_timeout_is_reported(kivi):
     oracle_step(1)
     _compare_all(st, cache, "after the reset")
     assert_close(out.cpu().numpy(), st.decode_ref(lens + 2), "fused step after the reset")
+
+
+def test_write_decode_up_to_table_capacity(kivi):
+    """The fused step up to exactly the block table's capacity: tables cut to
+    (max_seq_len - R) / page entries, so the last step of sequence 0 ages the
+    group that fills the table's last pages (255 -> 256 = max_seq_len)."""
+    w = wl.WORKLOADS["qwen14b"].scaled(batch=2, ctx_lo=200)
+    lens = np.array([250, 200])
+    steps = 6
+    st = State(w, lens=lens, extra_tokens=steps, seed=81)
+    mp = (256 - w.residual) // w.page  # 8 pages of 16: max_seq_len 256
+    st.tables = np.ascontiguousarray(st.tables[:, :mp])
+    st.max_pages = mp
+    st.geo = geometry(w, mp)
+    st.cache = o.Cache.empty(st.geo, st.num_pages, st.batch)
+    st.build_oracle()
+    geo = kivi.KiviGeometry(w.nh, w.nkv, w.hd, w.page, 32, w.residual, mp, st.num_pages)
+    assert geo.max_seq_len() == 256
+    cache = kivi.PagedKiviCache.from_tensors(geo, to_torch(st))
+    bt = torch.from_numpy(st.tables).cuda()
+    q = torch.from_numpy(st.q).view(torch.float16).cuda()
+    cur = lens.copy()
+    for s in range(steps):
+        nk = torch.stack([torch.from_numpy(st.k_hist[b][cur[b]].copy())
+                          for b in range(2)]).view(torch.float16).cuda()
+        nv = torch.stack([torch.from_numpy(st.v_hist[b][cur[b]].copy())
+                          for b in range(2)]).view(torch.float16).cuda()
+        after = cur + 1
+        out = cache.write_decode(q, nk, nv, torch.from_numpy(after.astype(np.int32)).cuda(), bt)
+        for b in range(2):
+            o.cache_write(st.cache, b, st.k_hist[b][cur[b]], st.v_hist[b][cur[b]], st.tables[b],
+                          int(after[b]))
+        cur = after
+        torch.cuda.synchronize()
+        _compare_all(st, cache, f"step {s}")
+        assert_close(out.cpu().numpy(), st.decode_ref(cur), f"capacity step {s}")
+    assert int(cur[0]) == geo.max_seq_len()
